@@ -1,0 +1,144 @@
+/*
+ * llmhip_sampler.h — C ABI of the MI355X (gfx950) decode-time sampler.
+ *
+ * Drop-in for scriptonait's CPU sampler:
+ *   pub fn sample_with(logits: &[f32], sampling: &SamplingConfig,
+ *                      recent: &[u32], rng: &mut Rng) -> u32
+ *   (crates/llm-core/src/generate.rs:325-420)
+ * batched over B rows. Per row it computes exactly what that function
+ * computes: allowed-mask -> repetition penalty over the history -> greedy
+ * exit -> temperature -> sort (value desc, id asc) -> top-k -> softmax over
+ * the top-k set -> min-p -> top-p -> seeded inverse-CDF draw, and returns
+ * the same token id. The reference has no FFI of its own (it is a plain
+ * Rust function); a Rust host binds these symbols through the `extern "C"`
+ * block shown in the integration notes, and falls back to `sample_with`
+ * when a call returns non-zero, as the WebGPU path falls back to the CPU
+ * (crates/wasm-app/src/inference.rs:204-214).
+ *
+ * Conventions
+ *   - Plain pointers and sizes only. The caller owns every buffer; the
+ *     library never frees caller memory.
+ *   - Every entry point returns an int status: LLMHIP_OK (0) or a negative
+ *     LLMHIP_ERR_* code. Nothing aborts. A degenerate row (all -inf after
+ *     masking, non-finite softmax sum) is not an error: it returns the
+ *     reference's fallback id, as sample_with does.
+ *   - RNG: rng_state[b] is the SplitMix64 state of row b
+ *     (crates/llm-core/src/rng.rs:6-22, `Rng::seed_from_u64(seed)` sets it to
+ *     `seed`). It is advanced by exactly one step for every row that draws
+ *     and left untouched for greedy and degenerate rows, as `Rng` is.
+ *   - Not thread-safe per context: one context per host thread. Calls on
+ *     one context are serialized on the stream they are given.
+ */
+#ifndef LLMHIP_SAMPLER_H
+#define LLMHIP_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLMHIP_ABI_VERSION 1
+
+enum {
+  LLMHIP_OK = 0,
+  LLMHIP_ERR_INVALID_ARGUMENT = -1, /* null pointer, ld < V, bad sizes */
+  LLMHIP_ERR_NO_DEVICE = -2,        /* no HIP device / device index out of range */
+  LLMHIP_ERR_HIP = -3,              /* a HIP runtime call failed (see llmhip_last_error) */
+  LLMHIP_ERR_OUT_OF_MEMORY = -4,    /* device scratch could not be allocated */
+  LLMHIP_ERR_UNSUPPORTED = -5       /* shape outside what this build handles */
+};
+
+/*
+ * Per-row sampling parameters: the numeric fields of SamplingConfig
+ * (crates/llm-core/src/generate.rs:25-80). `repetition_window` stays with
+ * the caller (it decides how much history to pass, generate.rs:178-182),
+ * `seed` is the initial rng_state, and `allowed` is passed separately.
+ */
+typedef struct llmhip_params {
+  float temperature;        /* <= 0 means greedy (argmax, no draw) */
+  uint32_t top_k;           /* 0 disables */
+  float top_p;              /* >= 1 disables */
+  float min_p;              /* <= 0 disables */
+  float repetition_penalty; /* == 1 disables (history is then not read) */
+} llmhip_params;
+
+typedef struct llmhip_ctx llmhip_ctx;
+
+/* Library ABI version (LLMHIP_ABI_VERSION of the build). No reference
+ * counterpart. */
+int llmhip_abi_version(void);
+
+/* Human-readable text for a status code. No reference counterpart. */
+const char* llmhip_status_string(int status);
+
+/* Text of the last HIP error seen on this thread, or "". */
+const char* llmhip_last_error(void);
+
+/* Create a context bound to HIP device `device`. The context owns the
+ * device scratch reused across calls (the reference allocates a Vec per
+ * call, generate.rs:331 and :364; here nothing is allocated in steady
+ * state). */
+int llmhip_ctx_create(int device, llmhip_ctx** out_ctx);
+
+/* Destroy a context and release its scratch. Null is accepted. */
+int llmhip_ctx_destroy(llmhip_ctx* ctx);
+
+/*
+ * Batched sample_with on HOST buffers (replaces generate.rs:325-420 at its
+ * call sites generate.rs:159 and crates/wasm-app/src/inference.rs:327).
+ * Copies the inputs to the device, runs the kernels, copies the results
+ * back and synchronizes before returning, so results are visible like the
+ * reference's return value.
+ *
+ *   logits        [B][ld] f32, row b's V logits start at logits + b*ld (ld >= V)
+ *   params        one llmhip_params per row, params[b * params_stride];
+ *                 params_stride == 0 shares params[0] across all rows
+ *   hist          concatenated token histories (`recent`), u32 ids; ids >= V
+ *                 are ignored, as work.get_mut(id) ignores them
+ *   hist_offsets  [B+1] CSR offsets: row b's history is
+ *                 hist[hist_offsets[b] .. hist_offsets[b+1]); both may be
+ *                 null for "no history"
+ *   allowed       nullable [allowed_len] u8 mask shared by all rows
+ *                 (SamplingConfig::allowed); ids >= allowed_len and eos_id
+ *                 are always allowed
+ *   eos_id        the end-of-text id (tokenizer::EOS = 258,
+ *                 crates/llm-core/src/tokenizer.rs:38)
+ *   rng_state     [B] u64 in/out
+ *   out_ids       [B] u32 sampled ids
+ *   out_probs     nullable [B][V] f32: post-truncation probabilities
+ *                 scattered by id (the `probs` the draw walks over,
+ *                 normalized over the top-k set), zero elsewhere; debug
+ *                 output, costs an extra B*V*4 bytes of writes
+ *   out_kept      nullable [B] u32: number of candidates the draw walked
+ *                 over (0 for greedy and degenerate rows)
+ */
+int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                       const llmhip_params* params, size_t params_stride,
+                       const uint32_t* hist, const uint32_t* hist_offsets,
+                       const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
+                       uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                       uint32_t* out_kept);
+
+/*
+ * The same computation on DEVICE buffers (all pointers are device
+ * pointers, same meaning as above), stream-ordered on `stream` (a
+ * hipStream_t; null = the default stream). Returns after enqueueing; the
+ * results are ready when the stream reaches that point. For decode loops
+ * whose logits, history and RNG state already live in HBM: nothing crosses
+ * PCIe. Scratch comes from the context (grown on first use of a larger
+ * shape, which is the only time this call allocates).
+ */
+int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                         const llmhip_params* params, size_t params_stride,
+                         const uint32_t* hist, const uint32_t* hist_offsets,
+                         const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
+                         uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                         uint32_t* out_kept, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMHIP_SAMPLER_H */

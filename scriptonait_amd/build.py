@@ -1,0 +1,78 @@
+"""Build step for the gfx950 sampler library (libllmhip_sampler.so).
+
+Compiles the HIP sources under csrc/ with hipcc for gfx950 only, in-tree,
+so the built library travels with the source tree. Flags that matter for
+parity with the reference's f32 arithmetic:
+
+* ``-ffp-contract=off``: no fused multiply-adds in f32 code (the reference's
+  Rust code rounds every operation); the exp routine asks for its fused
+  double-precision steps explicitly with __builtin_fma.
+* ``-fhip-fp32-correctly-rounded-divide-sqrt``: IEEE division, as Rust's
+  ``/`` on f32.
+* no fast-math.
+* ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed f32
+  instructions are generated.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+LIB_NAME = "libllmhip_sampler.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+SOURCES = ["sampler_kernels.hip", "sampler_api.hip"]
+ARCH = "gfx950"
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build the sampler)")
+
+
+def compile_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-ffp-contract=off",
+        "-fno-fast-math",
+        "-fhip-fp32-correctly-rounded-divide-sqrt",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall",
+        "-Wno-unused-result",
+    ]
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile every HIP source and link the shared library. Always rebuilds."""
+    hipcc = hipcc_path()
+    objs = []
+    for src in SOURCES:
+        obj = CSRC / (Path(src).stem + ".o")
+        cmd = [hipcc, *compile_flags(), "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        objs.append(str(obj))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB_PATH)
+    for o in objs:
+        Path(o).unlink(missing_ok=True)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build_library(verbose="-v" in sys.argv)
+    print(LIB_PATH)

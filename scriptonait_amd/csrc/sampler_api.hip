@@ -1,0 +1,335 @@
+// C ABI of the gfx950 sampler (declared in include/llmhip_sampler.h):
+// argument validation, the per-context device scratch, host<->device
+// staging for the host entry, and the choice of kernels for a batch.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+#include "sampler_common.h"
+
+namespace llmhip {
+hipError_t launch_fast(const SampleArgs& a, bool aligned, hipStream_t s);
+hipError_t launch_general(const SampleArgs& a, hipStream_t s);
+}  // namespace llmhip
+
+using namespace llmhip;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int hip_fail(hipError_t e, const char* what) {
+  char buf[256];
+  snprintf(buf, sizeof buf, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+  g_last_error = buf;
+  return e == hipErrorOutOfMemory ? LLMHIP_ERR_OUT_OF_MEMORY : LLMHIP_ERR_HIP;
+}
+
+int arg_fail(const char* what) {
+  g_last_error = what;
+  return LLMHIP_ERR_INVALID_ARGUMENT;
+}
+
+#define HIP_TRY(expr)                               \
+  do {                                              \
+    hipError_t e_ = (expr);                         \
+    if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+  } while (0)
+
+// A device buffer that only grows.
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  int ensure(size_t bytes) {
+    if (bytes <= cap) return LLMHIP_OK;
+    if (ptr) {
+      hipError_t e = hipFree(ptr);
+      ptr = nullptr;
+      cap = 0;
+      if (e != hipSuccess) return hip_fail(e, "hipFree");
+    }
+    size_t want = std::max<size_t>(bytes, 256);
+    hipError_t e = hipMalloc(&ptr, want);
+    if (e != hipSuccess) {
+      ptr = nullptr;
+      return hip_fail(e, "hipMalloc");
+    }
+    cap = want;
+    return LLMHIP_OK;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+  }
+};
+
+}  // namespace
+
+struct llmhip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;  // used by the host entry
+  DevBuf scratch;                // general-path per-row scratch
+  DevBuf params;                 // per-row params copied from the host
+  // staging of the host entry
+  DevBuf logits, hist, hoff, allowed, rng, ids, probs, kept;
+};
+
+namespace {
+
+struct Device {
+  int prev = -1;
+  bool ok = false;
+  explicit Device(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~Device() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+int validate(size_t B, size_t V, size_t ld, const float* logits, const llmhip_params* params,
+             const uint32_t* hist, const uint32_t* hist_offsets, const uint8_t* allowed,
+             size_t allowed_len, const uint64_t* rng_state, const uint32_t* out_ids) {
+  if (B == 0) return LLMHIP_OK;
+  if (!params) return arg_fail("params is null");
+  if (!rng_state || !out_ids) return arg_fail("rng_state and out_ids are required");
+  if (V > 0x7fffffffu) return arg_fail("V must be below 2^31");
+  if (B > 0x7fffffffu) return arg_fail("B must be below 2^31");
+  if (V > 0 && !logits) return arg_fail("logits is null");
+  if (ld < V) return arg_fail("ld < V");
+  if ((hist == nullptr) != (hist_offsets == nullptr)) return arg_fail("hist and hist_offsets go together");
+  if (allowed_len > 0 && !allowed) return arg_fail("allowed is null but allowed_len > 0");
+  if (allowed_len > 0xffffffffu) return arg_fail("allowed_len too large");
+  return LLMHIP_OK;
+}
+
+// Enqueue the kernels for one batch whose buffers are all on the device.
+// `params_host` is read on the host to choose kernels; `params_dev` is its
+// device copy (null when params_stride == 0).
+int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+            const llmhip_params* params_host, size_t params_stride, const llmhip_params* params_dev,
+            const uint32_t* hist, const uint32_t* hist_offsets, const uint8_t* allowed,
+            size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
+            float* out_probs, uint32_t* out_kept, hipStream_t s) {
+  if (V == 0) {
+    // Empty logits: sample_with returns 0 without drawing (generate.rs:375-377).
+    HIP_TRY(hipMemsetAsync(out_ids, 0, B * sizeof(uint32_t), s));
+    if (out_kept) HIP_TRY(hipMemsetAsync(out_kept, 0, B * sizeof(uint32_t), s));
+    return LLMHIP_OK;
+  }
+  uint32_t classes = 0;
+  if (params_stride == 0) {
+    classes = row_class(params_host[0], (uint32_t)V);
+  } else {
+    for (size_t b = 0; b < B; ++b) classes |= row_class(params_host[b * params_stride], (uint32_t)V);
+  }
+  const bool fast_ok = V <= kMaxFastV;
+  const uint32_t fast_mask = fast_ok ? (classes & (kClassGreedy | kClassTopK)) : 0u;
+  const uint32_t general_mask = classes & ~fast_mask;
+
+  // The fast kernel may hand a row to the general path, so scratch is
+  // always sized for the batch.
+  const size_t Vp = (V + kBlock - 1) / kBlock * kBlock;
+  const size_t row_words = 5 * Vp;
+  int st = ctx->scratch.ensure(B * row_words * sizeof(uint32_t));
+  if (st) return st;
+
+  SampleArgs a{};
+  a.logits = logits;
+  a.ld = ld;
+  a.V = (uint32_t)V;
+  a.B = (uint32_t)B;
+  a.params = params_stride ? params_dev : nullptr;
+  a.params_stride = (uint32_t)params_stride;
+  a.shared = params_host[0];
+  a.hist = hist;
+  a.hist_offsets = hist_offsets;
+  a.allowed = allowed_len ? allowed : nullptr;
+  a.allowed_len = (uint32_t)allowed_len;
+  a.eos_id = eos_id;
+  a.rng_state = rng_state;
+  a.out_ids = out_ids;
+  a.out_probs = out_probs;
+  a.out_kept = out_kept;
+  a.scratch = static_cast<uint32_t*>(ctx->scratch.ptr);
+  a.scratch_row_words = row_words;
+
+  if (out_probs) HIP_TRY(hipMemsetAsync(out_probs, 0, B * V * sizeof(float), s));
+  const bool aligned = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0);
+  if (fast_mask) {
+    a.row_class_mask = fast_mask;
+    HIP_TRY(launch_fast(a, aligned, s));
+  }
+  if (general_mask) {
+    a.row_class_mask = general_mask;
+    HIP_TRY(launch_general(a, s));
+  }
+  return LLMHIP_OK;
+}
+
+int copy_params(llmhip_ctx* ctx, const llmhip_params* params, size_t B, size_t params_stride,
+                const llmhip_params** out_dev, hipStream_t s) {
+  *out_dev = nullptr;
+  if (params_stride == 0) return LLMHIP_OK;
+  const size_t bytes = ((B - 1) * params_stride + 1) * sizeof(llmhip_params);
+  int st = ctx->params.ensure(bytes);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(ctx->params.ptr, params, bytes, hipMemcpyHostToDevice, s));
+  *out_dev = static_cast<const llmhip_params*>(ctx->params.ptr);
+  return LLMHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmhip_abi_version(void) { return LLMHIP_ABI_VERSION; }
+
+const char* llmhip_status_string(int status) {
+  switch (status) {
+    case LLMHIP_OK: return "ok";
+    case LLMHIP_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case LLMHIP_ERR_NO_DEVICE: return "no HIP device";
+    case LLMHIP_ERR_HIP: return "HIP runtime error";
+    case LLMHIP_ERR_OUT_OF_MEMORY: return "out of device memory";
+    case LLMHIP_ERR_UNSUPPORTED: return "unsupported shape";
+    default: return "unknown status";
+  }
+}
+
+const char* llmhip_last_error(void) { return g_last_error.c_str(); }
+
+int llmhip_ctx_create(int device, llmhip_ctx** out_ctx) {
+  if (!out_ctx) return arg_fail("out_ctx is null");
+  *out_ctx = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) {
+    g_last_error = "no HIP device";
+    return LLMHIP_ERR_NO_DEVICE;
+  }
+  if (device < 0 || device >= n) {
+    g_last_error = "device index out of range";
+    return LLMHIP_ERR_NO_DEVICE;
+  }
+  Device d(device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  llmhip_ctx* ctx = new llmhip_ctx();
+  ctx->device = device;
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_fail(e, "hipStreamCreateWithFlags");
+  }
+  *out_ctx = ctx;
+  return LLMHIP_OK;
+}
+
+int llmhip_ctx_destroy(llmhip_ctx* ctx) {
+  if (!ctx) return LLMHIP_OK;
+  Device d(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  (void)hipDeviceSynchronize();
+  for (DevBuf* b : {&ctx->scratch, &ctx->params, &ctx->logits, &ctx->hist, &ctx->hoff,
+                    &ctx->allowed, &ctx->rng, &ctx->ids, &ctx->probs, &ctx->kept})
+    b->release();
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return LLMHIP_OK;
+}
+
+int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                         const llmhip_params* params, size_t params_stride,
+                         const uint32_t* hist, const uint32_t* hist_offsets,
+                         const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
+                         uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                         uint32_t* out_kept, void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  int st = validate(B, V, ld, logits, params, hist, hist_offsets, allowed, allowed_len, rng_state,
+                    out_ids);
+  if (st || B == 0) return st;
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const llmhip_params* pdev = nullptr;
+  st = copy_params(ctx, params, B, params_stride, &pdev, s);
+  if (st) return st;
+  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, allowed,
+                 allowed_len, eos_id, rng_state, out_ids, out_probs, out_kept, s);
+}
+
+int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                       const llmhip_params* params, size_t params_stride,
+                       const uint32_t* hist, const uint32_t* hist_offsets,
+                       const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
+                       uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                       uint32_t* out_kept) {
+  if (!ctx) return arg_fail("ctx is null");
+  int st = validate(B, V, ld, logits, params, hist, hist_offsets, allowed, allowed_len, rng_state,
+                    out_ids);
+  if (st || B == 0) return st;
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = ctx->stream;
+
+  // Rows are copied densely (ld = V on the device).
+  const size_t nlog = B * V;
+  const size_t nhist = hist ? (size_t)hist_offsets[B] : 0;
+  if (hist && hist_offsets[0] != 0) return arg_fail("hist_offsets[0] must be 0");
+  for (size_t b = 0; hist && b < B; ++b)
+    if (hist_offsets[b + 1] < hist_offsets[b]) return arg_fail("hist_offsets must be non-decreasing");
+  if ((st = ctx->logits.ensure(nlog * sizeof(float)))) return st;
+  if ((st = ctx->rng.ensure(B * sizeof(uint64_t)))) return st;
+  if ((st = ctx->ids.ensure(B * sizeof(uint32_t)))) return st;
+  if (out_kept && (st = ctx->kept.ensure(B * sizeof(uint32_t)))) return st;
+  if (out_probs && (st = ctx->probs.ensure(nlog * sizeof(float)))) return st;
+  if (hist) {
+    if ((st = ctx->hist.ensure(std::max<size_t>(nhist, 1) * sizeof(uint32_t)))) return st;
+    if ((st = ctx->hoff.ensure((B + 1) * sizeof(uint32_t)))) return st;
+  }
+  if (allowed_len && (st = ctx->allowed.ensure(allowed_len))) return st;
+
+  float* dlog = static_cast<float*>(ctx->logits.ptr);
+  if (V > 0) {
+    if (ld == V) {
+      HIP_TRY(hipMemcpyAsync(dlog, logits, nlog * sizeof(float), hipMemcpyHostToDevice, s));
+    } else {
+      HIP_TRY(hipMemcpy2DAsync(dlog, V * sizeof(float), logits, ld * sizeof(float), V * sizeof(float), B,
+                               hipMemcpyHostToDevice, s));
+    }
+  }
+  HIP_TRY(hipMemcpyAsync(ctx->rng.ptr, rng_state, B * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+  if (hist) {
+    if (nhist) HIP_TRY(hipMemcpyAsync(ctx->hist.ptr, hist, nhist * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(ctx->hoff.ptr, hist_offsets, (B + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+  }
+  if (allowed_len) HIP_TRY(hipMemcpyAsync(ctx->allowed.ptr, allowed, allowed_len, hipMemcpyHostToDevice, s));
+  const llmhip_params* pdev = nullptr;
+  if ((st = copy_params(ctx, params, B, params_stride, &pdev, s))) return st;
+
+  st = enqueue(ctx, dlog, B, V, V, params, params_stride, pdev,
+               hist ? static_cast<const uint32_t*>(ctx->hist.ptr) : nullptr,
+               hist ? static_cast<const uint32_t*>(ctx->hoff.ptr) : nullptr,
+               allowed_len ? static_cast<const uint8_t*>(ctx->allowed.ptr) : nullptr, allowed_len,
+               eos_id, static_cast<uint64_t*>(ctx->rng.ptr), static_cast<uint32_t*>(ctx->ids.ptr),
+               out_probs ? static_cast<float*>(ctx->probs.ptr) : nullptr,
+               out_kept ? static_cast<uint32_t*>(ctx->kept.ptr) : nullptr, s);
+  if (st) {
+    (void)hipStreamSynchronize(s);
+    return st;
+  }
+  HIP_TRY(hipMemcpyAsync(out_ids, ctx->ids.ptr, B * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(rng_state, ctx->rng.ptr, B * sizeof(uint64_t), hipMemcpyDeviceToHost, s));
+  if (out_kept) HIP_TRY(hipMemcpyAsync(out_kept, ctx->kept.ptr, B * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  if (out_probs) HIP_TRY(hipMemcpyAsync(out_probs, ctx->probs.ptr, nlog * sizeof(float), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return LLMHIP_OK;
+}
+
+}  // extern "C"

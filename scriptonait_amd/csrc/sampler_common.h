@@ -1,0 +1,84 @@
+// Shared definitions of the gfx950 sampler: the SplitMix64 step, the
+// order-preserving key transform and the argument block the kernels take.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/llmhip_sampler.h"
+#include "glibc_expf.h"
+
+namespace llmhip {
+
+// crates/llm-core/src/rng.rs:16-22 (SplitMix64, one step).
+__host__ __device__ __forceinline__ uint64_t splitmix64_next(uint64_t& state) {
+  state += 0x9E3779B97F4A7C15ull;
+  uint64_t z = state;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// crates/llm-core/src/rng.rs:31-34: top 24 bits / 2^24 (exact in binary32).
+__host__ __device__ __forceinline__ float next_f32(uint64_t& state) {
+  return (float)(uint32_t)(splitmix64_next(state) >> 40) * 0x1p-24f;
+}
+
+// Order-preserving map from binary32 to u32: key(a) > key(b) iff a > b as
+// the reference's sort sees them (partial_cmp: -0.0 == +0.0). NaN maps to 0,
+// below every number (the reference's comparator is not a total order with
+// NaN; rows holding NaN are outside parity).
+__device__ __forceinline__ uint32_t f2key(float w) {
+  uint32_t u = __float_as_uint(w);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0u;
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+  if (k == 0u) return __uint_as_float(0x7fc00000u);
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+// One call's worth of arguments, passed by value to every kernel.
+struct SampleArgs {
+  const float* logits;
+  uint64_t ld;
+  uint32_t V;
+  uint32_t B;
+  const llmhip_params* params;  // device, per row (params_stride apart), or null
+  uint32_t params_stride;
+  llmhip_params shared;          // used when params == null
+  const uint32_t* hist;          // device, may be null
+  const uint32_t* hist_offsets;  // device [B+1], may be null
+  const uint8_t* allowed;        // device, may be null
+  uint32_t allowed_len;
+  uint32_t eos_id;
+  uint64_t* rng_state;
+  uint32_t* out_ids;
+  float* out_probs;    // may be null
+  uint32_t* out_kept;  // may be null
+  uint32_t* scratch;   // general path: per-row words
+  uint64_t scratch_row_words;
+  uint32_t row_class_mask;  // which row classes this launch handles
+};
+
+enum RowClass : uint32_t {
+  kClassGreedy = 1u,  // temperature <= 0
+  kClassTopK = 2u,    // 0 < top_k < V and top_k <= kMaxFastK
+  kClassFull = 4u,    // everything else (top_k == 0, top_k >= V, large top_k)
+};
+
+constexpr uint32_t kBlock = 1024;
+constexpr uint32_t kWaves = kBlock / 64;
+constexpr uint32_t kMaxFastK = 1024;     // largest top_k of the register path
+constexpr uint32_t kMaxFastV = 32768;    // largest V of the register path
+constexpr uint32_t kCandCap = 4096;      // candidate buffer of the register path
+
+__host__ __device__ __forceinline__ uint32_t row_class(const llmhip_params& p, uint32_t V) {
+  // generate.rs:354: `temperature <= 0.0` (a NaN temperature is not greedy).
+  if (p.temperature <= 0.0f) return kClassGreedy;
+  if (p.top_k > 0 && p.top_k < V && p.top_k <= kMaxFastK) return kClassTopK;
+  return kClassFull;
+}
+
+}  // namespace llmhip

@@ -1,0 +1,68 @@
+// Wavefront (64-lane) building blocks for gfx950.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmhip {
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (uint32_t off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
+#pragma unroll
+  for (uint32_t off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+#pragma unroll
+  for (uint32_t off = 32; off > 0; off >>= 1) {
+    const uint32_t y = __shfl_xor(x, off, 64);
+    x = y > x ? y : x;
+  }
+  return x;
+}
+
+// Value of `x` held by lane `l` (l uniform across the wave).
+__device__ __forceinline__ float readlane_f32(float x, uint32_t l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), (int)l));
+}
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, uint32_t l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, (int)l);
+}
+
+// Bit mask of the lanes below this one.
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const uint32_t lane = lane_id();
+  return lane == 0 ? 0ull : (~0ull >> (64u - lane));
+}
+
+// "Better" for the greedy argmax (crates/llm-core/src/ops/loss.rs:6-16):
+// larger value wins; equal values keep the smaller index.
+__device__ __forceinline__ void argmax_combine(float& bv, uint32_t& bi, float ov, uint32_t oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+__device__ __forceinline__ void wave_argmax(float& bv, uint32_t& bi) {
+#pragma unroll
+  for (uint32_t off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const uint32_t oi = __shfl_xor(bi, off, 64);
+    argmax_combine(bv, bi, ov, oi);
+  }
+}
+
+}  // namespace llmhip

@@ -1,0 +1,95 @@
+"""GPU parity: the HIP sampler against the CPU oracle on the same bytes.
+
+Configs 1-3 run at their full BASELINE sizes; configs 4-5 (the full-vocab
+path) at reduced batch here and at full size in test_gpu_full_sizes.py.
+"""
+import numpy as np
+import pytest
+
+from parity_util import compare, run_both
+from scriptonait_amd.workloads import PARAMS_DTYPE, make_params, make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_configs_full_size(sampler, cfg):
+    w = make_workload(cfg)
+    g, o = run_both(sampler, w)
+    s = compare(g, o, w.name)
+    print(w.name, s, flush=True)
+
+
+@pytest.mark.parametrize("cfg,B", [(4, 16), (5, 8)])
+def test_full_vocab_configs_reduced_batch(sampler, cfg, B):
+    w = make_workload(cfg, B=B)
+    g, o = run_both(sampler, w)
+    s = compare(g, o, w.name)
+    print(w.name, s, flush=True)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_other_data_seeds_config3(sampler, seed):
+    w = make_workload(3, data_seed=seed, B=64)
+    g, o = run_both(sampler, w)
+    compare(g, o, f"config3 seed {seed}")
+
+
+def test_greedy_rows(sampler):
+    w = make_workload(3, B=32)
+    prm = make_params(0.0, 64, 0.95, 0.05, 1.15)
+    g, o = run_both(sampler, w, params=prm)
+    assert np.array_equal(g.ids, o.ids)
+    assert np.array_equal(g.rng_state, w.rng_seeds), "greedy rows must not advance the RNG"
+
+
+def test_per_row_mixed_params(sampler):
+    w = make_workload(2, B=48)
+    prm = np.zeros(48, dtype=PARAMS_DTYPE)
+    for b in range(48):
+        kind = b % 6
+        prm[b] = [(0.0, 50, 0.9, 0.1, 1.2), (1.0, 50, 0.9, 0.1, 1.2), (0.7, 1, 1.0, 0.0, 1.0),
+                  (1.3, 0, 0.9, 0.0, 1.1), (1.0, 8192, 1.0, 0.2, 1.0), (0.5, 1000, 0.5, 0.0, 0.8)][kind]
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, "mixed per-row params")
+
+
+def test_allowed_mask(sampler):
+    w = make_workload(2, B=16)
+    allowed = np.ones(w.V - 100, dtype=np.uint8)  # ids past the mask stay allowed
+    allowed[::3] = 0
+    allowed[258] = 0  # EOS is always allowed
+    g, o = run_both(sampler, w, allowed=allowed)
+    compare(g, o, "allowed mask")
+
+
+@pytest.mark.parametrize("V", [1, 5, 7, 64, 257, 1000, 4097, 12345])
+def test_odd_vocab_sizes(sampler, V):
+    w = make_workload(3, B=6, V=V)
+    for k in (1, 3, 40):
+        prm = make_params(0.8, k, 0.95, 0.05, 1.1)
+        g, o = run_both(sampler, w, params=prm)
+        compare(g, o, f"V={V} k={k}")
+
+
+def test_all_masked_row_is_degenerate(sampler):
+    V = 300
+    logits = np.full((2, V), -np.inf, dtype=np.float32)
+    prm = make_params(0.9, 40, 0.95, 0.0, 1.1)
+    seeds = np.array([5, 6], dtype=np.uint64)
+    g = sampler.sample_host(logits, prm, seeds)
+    assert list(g.ids) == [0, 0]
+    assert np.array_equal(g.rng_state, seeds), "degenerate rows must not draw"
+
+
+def test_ties_resolve_by_smallest_id(sampler):
+    V = 2048
+    logits = np.zeros((4, V), dtype=np.float32)  # every value tied
+    prm = make_params(1.0, 5, 1.0, 0.0, 1.0)
+    seeds = np.arange(4, dtype=np.uint64)
+    from oracle import oracle
+
+    g = sampler.sample_host(logits, prm, seeds, want_probs=True)
+    o = oracle.sample_batch(logits, prm, seeds, want_probs=True)
+    assert np.array_equal(g.ids, o.ids)
+    assert set(g.ids.tolist()) <= {0, 1, 2, 3, 4}
