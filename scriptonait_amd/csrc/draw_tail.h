@@ -13,14 +13,6 @@
 
 namespace llmhip {
 
-// Result of the tail for one row.
-struct TailResult {
-  uint32_t pick;  // index into the sorted candidate list
-  uint32_t kept;  // candidates the draw walked over (0 = degenerate exit)
-  float sum;      // softmax normalizer
-  float mx;       // max over the candidates
-};
-
 // key_at(i) / id_at(i): i-th candidate (i < n) in sorted order.
 // Must be called by all 64 lanes of exactly one wave. Writes out_ids,
 // rng_state, out_kept and (if requested) out_probs for row b.
@@ -31,7 +23,7 @@ __device__ void draw_tail(const SampleArgs& a, uint32_t b, const llmhip_params& 
   const uint32_t k0 = key_at(0);
   // fold(NEG_INFINITY, f32::max) over sorted candidates: the first one
   // unless it is NaN (NaN keys sort last, so then all are NaN).
-  const float mx = k0 == 0u ? -INFINITY : key2f(k0);
+  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
   auto e_at = [&](uint32_t i) { return glibc_expf(key2f(key_at(i)) - mx); };
 
   // generate.rs:374: sum as a left fold in sorted order.

@@ -24,17 +24,20 @@ __host__ __device__ __forceinline__ float next_f32(uint64_t& state) {
 }
 
 // Order-preserving map from binary32 to u32: key(a) > key(b) iff a > b as
-// the reference's sort sees them (partial_cmp: -0.0 == +0.0). NaN maps to 0,
+// the reference's sort sees them (partial_cmp: -0.0 == +0.0). NaN maps to 1,
 // below every number (the reference's comparator is not a total order with
-// NaN; rows holding NaN are outside parity).
+// NaN; rows holding NaN are outside parity). Key 0 is reserved for "no
+// element" (padding, or a logit handed to another lane).
+constexpr uint32_t kKeyNone = 0u;
+constexpr uint32_t kKeyNaN = 1u;
 __device__ __forceinline__ uint32_t f2key(float w) {
-  uint32_t u = __float_as_uint(w);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0u;
-  if (u == 0x80000000u) u = 0u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  uint32_t u = __float_as_uint(w + 0.0f);  // -0.0 + 0.0 == +0.0
+  const uint32_t flip = (uint32_t)((int32_t)u >> 31) | 0x80000000u;
+  u ^= flip;
+  return w == w ? u : kKeyNaN;
 }
 __device__ __forceinline__ float key2f(uint32_t k) {
-  if (k == 0u) return __uint_as_float(0x7fc00000u);
+  if (k <= kKeyNaN) return __uint_as_float(0x7fc00000u);
   const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
   return __uint_as_float(u);
 }
@@ -72,7 +75,6 @@ constexpr uint32_t kBlock = 1024;
 constexpr uint32_t kWaves = kBlock / 64;
 constexpr uint32_t kMaxFastK = 1024;     // largest top_k of the register path
 constexpr uint32_t kMaxFastV = 32768;    // largest V of the register path
-constexpr uint32_t kCandCap = 4096;      // candidate buffer of the register path
 
 __host__ __device__ __forceinline__ uint32_t row_class(const llmhip_params& p, uint32_t V) {
   // generate.rs:354: `temperature <= 0.0` (a NaN temperature is not greedy).

@@ -208,21 +208,46 @@ __global__ __launch_bounds__(kBlock) void sample_general_kernel(SampleArgs a) {
 // ---------------------------------------------------------------------------
 // Fast path: V <= 32768, row in registers.
 // ---------------------------------------------------------------------------
+
+// Workgroup barrier that orders LDS only: outstanding global loads stay in
+// flight across it (a full __syncthreads would wait for every logits load).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+constexpr uint32_t kMaxPen = 4096;    // distinct penalized ids per row (register path)
+constexpr uint32_t kFastCand = 2048;  // candidate buffer (register path)
+constexpr uint32_t kPenPerThread = kMaxPen / kBlock;
+
+// Element e of thread t holds position ((e/4)*1024 + t)*4 + e%4: each wave
+// reads 1 KiB contiguous per dwordx4 load. Position p lives in thread
+// (p/4) % 1024, slot ((p/4096)*4 + p%4).
+__device__ __forceinline__ uint32_t slot_pos(uint32_t e, uint32_t tid) {
+  return ((e >> 2) * kBlock + tid) * 4u + (e & 3u);
+}
+__device__ __forceinline__ uint32_t pos_owner(uint32_t p) { return (p >> 2) & (kBlock - 1); }
+__device__ __forceinline__ uint32_t pos_slot(uint32_t p) { return ((p >> 12) << 2) | (p & 3u); }
+
 template <int NCH, bool ALIGNED>
 __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
-  // u16 history multiplicities (2 per word); reused as the general-path LDS
-  // when a row falls back.
+  // u16 history multiplicity per id (2 per word); reused as the
+  // general-path LDS when a row falls back.
   __shared__ uint32_t s_cnt[kMaxFastV / 2];
+  __shared__ uint32_t s_pm[kBlock];      // per-thread mask of slots whose logit is penalized
+  __shared__ uint32_t s_plist[kMaxPen];  // distinct penalized ids
   __shared__ uint32_t s_hist[4 * 256];
-  __shared__ uint32_t s_ckey[kCandCap];
-  __shared__ uint32_t s_cid[kCandCap];
-  __shared__ uint32_t s_rank[kCandCap];
+  __shared__ uint32_t s_ckey[kFastCand];
+  __shared__ uint32_t s_cid[kFastCand];
+  __shared__ uint32_t s_rank[kFastCand];
   __shared__ uint32_t s_skey[kMaxFastK];
   __shared__ uint32_t s_sid[kMaxFastK];
   __shared__ float s_redv[kWaves];
   __shared__ uint32_t s_redi[kWaves];
-  __shared__ uint32_t s_misc[4];
+  __shared__ uint32_t s_misc[8];
   static_assert(sizeof(GenLds) <= sizeof(s_cnt), "general-path LDS must fit the count table");
+  static_assert(NCH * 4 <= 32, "slot mask is 32 bits");
 
   const uint32_t b = blockIdx.x;
   if (b >= a.B) return;
@@ -231,6 +256,7 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   const uint32_t V = a.V;
   const uint32_t cls = row_class(P, V);
   if (!(cls & a.row_class_mask)) return;
+  const float T = P.temperature, rp = P.repetition_penalty;
 
   bool use_pen = P.repetition_penalty != 1.0f && a.hist && a.hist_offsets;
   uint32_t h0 = 0, h1 = 0;
@@ -244,13 +270,15 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
       return;
     }
   }
-  // History ids first, so their LDS counting overlaps the logits loads.
+  // History ids are loaded before the logits so the counting below only
+  // waits for them, not for the row.
   uint32_t hid0 = 0xffffffffu, hid1 = 0xffffffffu;
   if (use_pen) {
     if (h0 + tid < h1) hid0 = a.hist[h0 + tid];
     if (h0 + kBlock + tid < h1) hid1 = a.hist[h0 + kBlock + tid];
   }
 
+  // All row loads in flight at once: NCH dwordx4 per lane.
   const float* row = a.logits + (size_t)b * a.ld;
   float x[NCH * 4];
 #pragma unroll
@@ -270,38 +298,81 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
 
   if (use_pen) {
     for (uint32_t i = tid; i < (V + 1) / 2; i += kBlock) s_cnt[i] = 0u;
+    s_pm[tid] = 0u;
   }
   s_hist[tid] = 0u;  // 4 x 256 bins == kBlock
-  if (tid == 0) s_misc[2] = 0u;
-  __syncthreads();
+  if (tid < 8) s_misc[tid] = 0u;
+  lds_barrier();
+
+  // History multiplicities (integer LDS atomics: the counts do not depend
+  // on the order). The first occurrence of an id enlists it for one
+  // processor lane and marks its slot in the owner's mask.
+  uint32_t D = 0;
   if (use_pen) {
-    if (hid0 < V) atomicAdd(&s_cnt[hid0 >> 1], 1u << ((hid0 & 1u) << 4));
-    if (hid1 < V) atomicAdd(&s_cnt[hid1 >> 1], 1u << ((hid1 & 1u) << 4));
-    for (uint32_t j = h0 + 2u * kBlock + tid; j < h1; j += kBlock) {
-      const uint32_t id = a.hist[j];
-      if (id < V) atomicAdd(&s_cnt[id >> 1], 1u << ((id & 1u) << 4));
+    auto add_hist = [&](uint32_t id) {
+      if (id < V) {
+        const uint32_t sh = (id & 1u) << 4;
+        const uint32_t old = atomicAdd(&s_cnt[id >> 1], 1u << sh);
+        if (((old >> sh) & 0xffffu) == 0u) {
+          const uint32_t q = atomicAdd(&s_misc[3], 1u);
+          if (q < kMaxPen) s_plist[q] = id;
+          atomicOr(&s_pm[pos_owner(id)], 1u << pos_slot(id));
+        }
+      }
+    };
+    add_hist(hid0);
+    add_hist(hid1);
+    for (uint32_t j = h0 + 2u * kBlock + tid; j < h1; j += kBlock) add_hist(a.hist[j]);
+    lds_barrier();
+    D = s_misc[3];
+    if (D > kMaxPen) {
+      __syncthreads();
+      general_row(a, b, P, *reinterpret_cast<GenLds*>(s_cnt));
+      return;
     }
-    __syncthreads();
   }
 
-  const float T = P.temperature, rp = P.repetition_penalty;
+  // Processor lanes: each distinct penalized id is gathered once (its line
+  // is being streamed by the row loads, so this merges in L2) and given
+  // mask -> penalty (m times in sequence: no float atomics) here.
+  float gv[kPenPerThread];
+  uint32_t gp[kPenPerThread], gm[kPenPerThread];
+#pragma unroll
+  for (uint32_t r = 0; r < kPenPerThread; ++r) {
+    const uint32_t q = tid + r * kBlock;
+    gp[r] = 0xffffffffu;
+    gm[r] = 0u;
+    gv[r] = 0.0f;
+    if (q < D) {
+      const uint32_t p = s_plist[q];
+      gp[r] = p;
+      gm[r] = (s_cnt[p >> 1] >> ((p & 1u) << 4)) & 0xffffu;
+      gv[r] = row[p];
+    }
+  }
+  const uint32_t pm = use_pen ? s_pm[tid] : 0u;
+
   if (cls == kClassGreedy) {
+    // ops/loss.rs:6-16 over the penalized, masked row (before temperature).
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
+    for (int e = 0; e < NCH * 4; ++e) {
+      const uint32_t pos = slot_pos(e, tid);
+      float v = x[e];
+      if (a.allowed && masked_out(a, pos)) v = -INFINITY;
+      if (pos < V && !((pm >> e) & 1u) && v > bv) {
+        bv = v;
+        bi = pos;
+      }
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t pos = ((uint32_t)c * kBlock + tid) * 4u + j;
-        if (pos < V) {
-          float v = x[4 * c + j];
-          if (masked_out(a, pos)) v = -INFINITY;
-          if (use_pen) v = apply_penalty(v, (s_cnt[pos >> 1] >> ((pos & 1u) << 4)) & 0xffffu, rp);
-          if (v > bv) {
-            bv = v;
-            bi = pos;
-          }
-        }
+    for (uint32_t r = 0; r < kPenPerThread; ++r) {
+      if (gp[r] != 0xffffffffu) {
+        float v = gv[r];
+        if (masked_out(a, gp[r])) v = -INFINITY;
+        v = apply_penalty(v, gm[r], rp);
+        if (v > -INFINITY) argmax_combine(bv, bi, v, gp[r]);
       }
     }
     const uint32_t w = block_argmax(bv, bi, s_redv, s_redi);
@@ -312,28 +383,37 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
     return;
   }
 
-  // mask -> penalty -> temperature -> key (generate.rs:333-359).
+  // Keys of the pre-temperature values v (mask applied; penalized logits
+  // are represented by their processor lane instead). Dividing by T > 0
+  // is monotone, so the top-k by v contains the top-k by v/T except for
+  // values that the division merges into ties; those are caught below.
   uint32_t key[NCH * 4];
-  uint32_t tmax = 0u;
+  uint32_t tmax = kKeyNone;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
+  for (int e = 0; e < NCH * 4; ++e) {
+    const uint32_t pos = slot_pos(e, tid);
+    float v = x[e];
+    if (a.allowed && masked_out(a, pos)) v = -INFINITY;
+    uint32_t k = f2key(v);
+    if (pos >= V || ((pm >> e) & 1u)) k = kKeyNone;
+    key[e] = k;
+    tmax = k > tmax ? k : tmax;
+  }
+  uint32_t gk[kPenPerThread];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t pos = ((uint32_t)c * kBlock + tid) * 4u + j;
-      uint32_t k = 0u;
-      if (pos < V) {
-        float v = x[4 * c + j];
-        if (masked_out(a, pos)) v = -INFINITY;
-        if (use_pen) v = apply_penalty(v, (s_cnt[pos >> 1] >> ((pos & 1u) << 4)) & 0xffffu, rp);
-        k = f2key(v / T);
-      }
-      key[4 * c + j] = k;
-      tmax = k > tmax ? k : tmax;
+  for (uint32_t r = 0; r < kPenPerThread; ++r) {
+    gk[r] = kKeyNone;
+    if (gp[r] != 0xffffffffu) {
+      float v = gv[r];
+      if (masked_out(a, gp[r])) v = -INFINITY;
+      gk[r] = f2key(apply_penalty(v, gm[r], rp));
+      tmax = gk[r] > tmax ? gk[r] : tmax;
     }
   }
 
-  // Exact K-th largest of the 1024 per-thread maxima, 4 x 8-bit LDS radix
-  // passes. Bins are scanned from the top by wave 0.
+  // tau = exact K-th largest of the 1024 per-thread maxima (4 x 8-bit LDS
+  // radix passes, bins scanned from the top by wave 0). At least K
+  // elements have key >= tau and they live in at most K threads.
   const uint32_t K = P.top_k;  // 0 < K < V, K <= 1024 (row class)
   uint32_t prefix = 0u, kk = K;
 #pragma unroll
@@ -341,7 +421,7 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
     const uint32_t shift = 24u - 8u * pass;
     const uint32_t hi_mask = pass == 0 ? 0u : (0xffffffffu << (shift + 8u));
     if ((tmax & hi_mask) == prefix) atomicAdd(&s_hist[pass * 256u + ((tmax >> shift) & 255u)], 1u);
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
       const uint32_t d0 = 255u - 4u * lane;
       const uint32_t* h = s_hist + pass * 256u;
@@ -349,7 +429,9 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
       const uint32_t tot = c0 + c1 + c2 + c3;
       const uint32_t incl = wave_incl_scan(tot);
       uint32_t cum = incl - tot;
-      if (cum < kk && kk <= incl) {
+      uint32_t np = 0u, nk = 0u;
+      const bool mine = cum < kk && kk <= incl;
+      if (mine) {
         uint32_t d;
         if (cum + c0 >= kk) {
           d = d0;
@@ -361,23 +443,56 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
           cum += c2;
           d = d0 - 3;
         }
-        s_misc[0] = prefix | (d << shift);
-        s_misc[1] = kk - cum;
+        np = prefix | (d << shift);
+        nk = kk - cum;
+      }
+      const uint64_t who = __ballot(mine);
+      const uint32_t src = who ? (uint32_t)__ffsll((unsigned long long)who) - 1u : 0u;
+      np = readlane_u32(np, src);
+      nk = readlane_u32(nk, src);
+      if (pass < 3) {
+        if (lane == 0) {
+          s_misc[0] = np;
+          s_misc[1] = nk;
+        }
+      } else {
+        // Lowest v key whose v/T equals (tau)/T: the candidate threshold.
+        // Lane l tests the value l+1 keys below tau; the run of ties from
+        // the top is at most ceil(2T)+1 long, so one wave covers T < 31.
+        uint32_t lo = np;
+        if (np > kKeyNaN + 64u) {
+          const uint32_t wt = f2key(key2f(np) / T);
+          const bool tie = f2key(key2f(np - 1u - lane) / T) == wt;
+          const uint64_t ties = __ballot(tie);
+          const uint64_t run = ~ties;
+          if (run == 0ull) {
+            lo = kKeyNaN;  // more than 64 tied values: take everything
+          } else {
+            lo = np - (uint32_t)(__ffsll((unsigned long long)run) - 1);
+          }
+        } else {
+          lo = kKeyNaN;
+        }
+        if (lane == 0) {
+          s_misc[0] = np;
+          s_misc[1] = lo;
+        }
       }
     }
-    __syncthreads();
+    lds_barrier();
     prefix = s_misc[0];
     kk = s_misc[1];
   }
-  const uint32_t tau = prefix;
+  // After the last pass s_misc[1] holds the threshold.
+  const uint32_t thr = kk > kKeyNaN ? kk : kKeyNaN;
 
-  // Append every element with key >= tau (one LDS atomic per wave).
+  // Append candidates (key >= thr) with their post-temperature key: one
+  // LDS atomic per wave, one division per candidate.
   uint32_t mine = 0u;
 #pragma unroll
-  for (int e = 0; e < NCH * 4; ++e) {
-    const uint32_t pos = ((uint32_t)(e >> 2) * kBlock + tid) * 4u + (e & 3);
-    mine += (pos < V && key[e] >= tau) ? 1u : 0u;
-  }
+  for (int e = 0; e < NCH * 4; ++e) mine += key[e] >= thr ? 1u : 0u;
+#pragma unroll
+  for (uint32_t r = 0; r < kPenPerThread; ++r) mine += gk[r] >= thr ? 1u : 0u;
   const uint32_t incl = wave_incl_scan(mine);
   const uint32_t wtot = readlane_u32(incl, 63);
   uint32_t wbase = 0u;
@@ -386,31 +501,41 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   uint32_t slot = wbase + incl - mine;
 #pragma unroll
   for (int e = 0; e < NCH * 4; ++e) {
-    const uint32_t pos = ((uint32_t)(e >> 2) * kBlock + tid) * 4u + (e & 3);
-    if (pos < V && key[e] >= tau) {
-      if (slot < kCandCap) {
-        s_ckey[slot] = key[e];
-        s_cid[slot] = pos;
+    if (key[e] >= thr) {
+      if (slot < kFastCand) {
+        s_ckey[slot] = f2key(key2f(key[e]) / T);
+        s_cid[slot] = slot_pos(e, tid);
       }
       ++slot;
     }
   }
-  __syncthreads();
+#pragma unroll
+  for (uint32_t r = 0; r < kPenPerThread; ++r) {
+    if (gk[r] >= thr) {
+      if (slot < kFastCand) {
+        s_ckey[slot] = f2key(key2f(gk[r]) / T);
+        s_cid[slot] = gp[r];
+      }
+      ++slot;
+    }
+  }
+  lds_barrier();
   const uint32_t n = s_misc[2];
-  if (n > kCandCap) {
+  if (n > kFastCand) {
     // Heavy ties at the threshold: not bounded by the register path.
     __syncthreads();
     general_row(a, b, P, *reinterpret_cast<GenLds*>(s_cnt));
     return;
   }
 
-  // Rank by (key desc, id asc): rank(i) = #{j : cand j precedes cand i}.
+  // Rank by (w key desc, id asc): rank(i) = #{j : cand j precedes cand i},
+  // the j range split over all waves.
   for (uint32_t i = tid; i < n; i += kBlock) s_rank[i] = 0u;
-  __syncthreads();
+  lds_barrier();
   if (n <= kBlock) {
     const uint32_t n64 = (n + 63u) & ~63u;
-    const uint32_t groups = kBlock / n64;
-    const uint32_t i = tid % n64, g = tid / n64;
+    const uint32_t groups = n64 ? kBlock / n64 : 1u;
+    const uint32_t i = n64 ? tid % n64 : 0u, g = n64 ? tid / n64 : 0u;
     if (g < groups && i < n) {
       const uint32_t ki = s_ckey[i], ii = s_cid[i];
       const uint32_t j0 = n * g / groups, j1 = n * (g + 1) / groups;
@@ -432,7 +557,7 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
       s_rank[i] = r;
     }
   }
-  __syncthreads();
+  lds_barrier();
   for (uint32_t i = tid; i < n; i += kBlock) {
     const uint32_t r = s_rank[i];
     if (r < K) {
@@ -440,7 +565,7 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
       s_sid[r] = s_cid[i];
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
     draw_tail(a, b, P, K, [&](uint32_t i) { return s_skey[i]; }, [&](uint32_t i) { return s_sid[i]; });
   }

@@ -93,3 +93,38 @@ def test_ties_resolve_by_smallest_id(sampler):
     o = oracle.sample_batch(logits, prm, seeds, want_probs=True)
     assert np.array_equal(g.ids, o.ids)
     assert set(g.ids.tolist()) <= {0, 1, 2, 3, 4}
+
+
+@pytest.mark.parametrize("T", [0.05, 0.3, 0.7, 1.7, 8.0, 30.0, 100.0])
+def test_temperatures_merge_ties(sampler, T):
+    """Division by T can merge distinct logits into equal values, which the
+    reference then orders by id; small and large T stress that boundary."""
+    w = make_workload(3, B=32)
+    prm = make_params(T, 64, 0.95, 0.05, 1.15)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, f"T={T}")
+
+
+def test_quantized_logits_many_ties(sampler):
+    """Logits on a coarse grid: thousands of exact ties around the top-k cut."""
+    w = make_workload(3, B=16)
+    w.logits[:] = np.round(w.logits * 4.0) / 4.0
+    for k in (1, 16, 64, 500):
+        prm = make_params(0.9, k, 0.97, 0.01, 1.1)
+        g, o = run_both(sampler, w, params=prm)
+        compare(g, o, f"quantized k={k}")
+
+
+def test_long_history_with_repeats(sampler):
+    """History longer than 2048 ids (loaded in the loop), heavy repeats."""
+    w = make_workload(3, B=8)
+    H = 5000
+    rs = np.random.default_rng(7)
+    hist = rs.integers(0, 50, size=8 * H).astype(np.uint32)  # ids repeat ~100 times
+    hist[::7] = rs.integers(0, w.V + 100, size=hist[::7].size)  # some ids >= V (ignored)
+    offs = (np.arange(9) * H).astype(np.uint32)
+    g = sampler.sample_host(w.logits, w.params, w.rng_seeds, hist, offs, V=w.V, want_probs=True)
+    from oracle import oracle
+
+    o = oracle.sample_batch(w.logits, w.params, w.rng_seeds, hist, offs, V=w.V, want_probs=True)
+    compare(g, o, "long history")
