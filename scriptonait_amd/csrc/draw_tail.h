@@ -17,7 +17,7 @@ namespace llmhip {
 // Must be called by all 64 lanes of exactly one wave. Writes out_ids,
 // rng_state, out_kept and (if requested) out_probs for row b.
 template <class KeyAt, class IdAt>
-__device__ void draw_tail(const SampleArgs& a, uint32_t b, const llmhip_params& P, uint32_t n,
+__device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const llmhip_params& P, uint32_t n,
                           KeyAt key_at, IdAt id_at) {
   const uint32_t lane = lane_id();
   const uint32_t k0 = key_at(0);
@@ -118,6 +118,119 @@ __device__ void draw_tail(const SampleArgs& a, uint32_t b, const llmhip_params& 
     float* prow = a.out_probs + (size_t)b * a.V;
     for (uint32_t i = lane; i < keep; i += 64) prow[id_at(i)] = p_at(i);
   }
+}
+
+// Same computation for n <= 64 candidates held one per lane (lane i holds
+// candidate i's key and id; lanes >= n are ignored), with the RNG state
+// already in a register. Each fold is a chain of dependent VGPR adds over
+// all 64 values, fetched from LDS (`buf`, 128 floats) into registers up
+// front; padding lanes contribute +0.0, which leaves an f32 sum of
+// non-negative terms unchanged. Running values are parked in LDS so that
+// lane i can test its own prefix, and a ballot finds the first lane that
+// decides (the reference's early `break`).
+__device__ __forceinline__ void draw_tail_small(const SampleArgs& a, uint32_t b, const llmhip_params& P,
+                                                uint32_t n, uint32_t my_key, uint32_t my_id,
+                                                uint64_t st, float* buf) {
+  const uint32_t lane = lane_id();
+  const bool act = lane < n;
+  const uint32_t k0 = readlane_u32(my_key, 0);
+  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
+  const float e = act ? glibc_expf(key2f(my_key) - mx) : 0.0f;
+  float* cbuf = buf + 64;
+  const float4* b4 = reinterpret_cast<const float4*>(buf);
+
+  // generate.rs:374
+  buf[lane] = e;
+  float sum = 0.0f;
+  {
+    float4 v[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = b4[q];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      sum += v[q].x;
+      sum += v[q].y;
+      sum += v[q].z;
+      sum += v[q].w;
+    }
+  }
+  // generate.rs:375-377
+  if (!(sum > 0.0f) || !isfinite(sum)) {
+    if (lane == 0) {
+      a.out_ids[b] = n > 0 ? my_id : 0u;
+      if (a.out_kept) a.out_kept[b] = 0u;
+    }
+    return;
+  }
+  const float p = act ? e / sum : 0.0f;  // generate.rs:378-380
+
+  // generate.rs:384-395
+  uint32_t keep = n;
+  if (P.min_p > 0.0f) {
+    const float thr = P.min_p * readlane_f32(p, 0);
+    const uint64_t fail = __ballot(act && !(p >= thr));
+    if (fail) keep = (uint32_t)__ffsll((unsigned long long)fail) - 1u;
+    if (keep < 1u) keep = 1u;
+  }
+
+  // generate.rs:397-411: c_i = fold of p_0..p_i; lane i reads its c_i. The
+  // total over a kept prefix is that fold at its last element.
+  buf[lane] = p;
+  float4 pv[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) pv[q] = b4[q];
+  {
+    float c = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      float4 o;
+      c += pv[q].x;
+      o.x = c;
+      c += pv[q].y;
+      o.y = c;
+      c += pv[q].z;
+      o.z = c;
+      c += pv[q].w;
+      o.w = c;
+      if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
+    }
+  }
+  const float my_c = lane < keep ? cbuf[lane] : 0.0f;
+  uint32_t stop = keep;
+  if (P.top_p < 1.0f) {
+    const uint64_t hit = __ballot(lane < keep && my_c >= P.top_p);
+    if (hit) stop = (uint32_t)__ffsll((unsigned long long)hit);
+  }
+  const float total = readlane_f32(my_c, stop - 1u);
+
+  // generate.rs:412-419: r_i = r before subtracting p_i; lane i tests r_i < p_i.
+  const float ur = next_f32(st);
+  {
+    float r = ur * total;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      float4 o;
+      o.x = r;
+      r -= pv[q].x;
+      o.y = r;
+      r -= pv[q].y;
+      o.z = r;
+      r -= pv[q].z;
+      o.w = r;
+      r -= pv[q].w;
+      if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
+    }
+  }
+  const float my_r = lane < stop ? cbuf[lane] : 0.0f;
+  const uint64_t hit = __ballot(lane < stop && my_r < p);
+  const uint32_t pick = hit ? (uint32_t)__ffsll((unsigned long long)hit) - 1u : stop - 1u;
+  const uint32_t id = readlane_u32(my_id, pick);
+  if (lane == 0) {
+    a.out_ids[b] = id;
+    a.rng_state[b] = st;
+    if (a.out_kept) a.out_kept[b] = stop;
+  }
+  if (a.out_probs && lane < stop) a.out_probs[(size_t)b * a.V + my_id] = p;
 }
 
 }  // namespace llmhip

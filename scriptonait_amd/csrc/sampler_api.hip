@@ -12,7 +12,7 @@
 #include "sampler_common.h"
 
 namespace llmhip {
-hipError_t launch_fast(const SampleArgs& a, bool aligned, hipStream_t s);
+hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s);
 hipError_t launch_general(const SampleArgs& a, hipStream_t s);
 }  // namespace llmhip
 
@@ -161,10 +161,12 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.scratch_row_words = row_words;
 
   if (out_probs) HIP_TRY(hipMemsetAsync(out_probs, 0, B * V * sizeof(float), s));
-  const bool aligned = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0);
+  // 128-bit row loads need 16-byte aligned rows and V % 4 == 0 (a row's
+  // last float4 must not extend past its V logits).
+  const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0) && (V % 4 == 0);
   if (fast_mask) {
     a.row_class_mask = fast_mask;
-    HIP_TRY(launch_fast(a, aligned, s));
+    HIP_TRY(launch_fast(a, vec, s));
   }
   if (general_mask) {
     a.row_class_mask = general_mask;

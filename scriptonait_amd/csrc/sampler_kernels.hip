@@ -37,8 +37,25 @@ struct GenLds {
   uint32_t redi[kWaves];
 };
 
+// Read-only inputs that every lane of a wave reads at the same address go
+// through the constant address space, so they become scalar (SMEM) loads:
+// those count on lgkmcnt and never queue behind the row's vector loads.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* as_const(const T* p) {
+  return (const __attribute__((address_space(4))) T*)p;
+}
+
 __device__ __forceinline__ llmhip_params load_params(const SampleArgs& a, uint32_t b) {
-  return a.params ? a.params[(size_t)b * a.params_stride] : a.shared;
+  llmhip_params P = a.shared;
+  if (a.params) {
+    const auto* q = as_const(a.params) + (size_t)b * a.params_stride;
+    P.temperature = q->temperature;
+    P.top_k = q->top_k;
+    P.top_p = q->top_p;
+    P.min_p = q->min_p;
+    P.repetition_penalty = q->repetition_penalty;
+  }
+  return P;
 }
 
 __device__ __forceinline__ float apply_penalty(float v, uint32_t m, float rp) {
@@ -73,7 +90,8 @@ __device__ __forceinline__ uint32_t block_argmax(float bv, uint32_t bi, float* r
 // General path: one row, 1024 threads, scratch in HBM.
 // Scratch per row (Vp = V rounded up to 1024): keysA | idsA | keysB | idsB | cnt
 // ---------------------------------------------------------------------------
-__device__ void general_row(const SampleArgs& a, uint32_t b, const llmhip_params& P, GenLds& L) {
+__device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, GenLds& L) {
+  const llmhip_params P = load_params(a, b);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t V = a.V;
   const uint32_t Vp = (V + kBlock - 1) / kBlock * kBlock;
@@ -200,9 +218,8 @@ __global__ __launch_bounds__(kBlock) void sample_general_kernel(SampleArgs a) {
   __shared__ GenLds L;
   const uint32_t b = blockIdx.x;
   if (b >= a.B) return;
-  const llmhip_params P = load_params(a, b);
-  if (!(row_class(P, a.V) & a.row_class_mask)) return;
-  general_row(a, b, P, L);
+  if (!(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  general_row(a, b, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -220,6 +237,10 @@ __device__ __forceinline__ void lds_barrier() {
 constexpr uint32_t kMaxPen = 4096;    // distinct penalized ids per row (register path)
 constexpr uint32_t kFastCand = 2048;  // candidate buffer (register path)
 constexpr uint32_t kPenPerThread = kMaxPen / kBlock;
+constexpr uint32_t kSelBits = 12;     // threshold histogram: top 12 key bits
+constexpr uint32_t kSelBins = 1u << kSelBits;
+constexpr uint32_t kHistWaves = 4;    // waves that load and count the history
+constexpr uint32_t kHistPerThread = 4;
 
 // Element e of thread t holds position ((e/4)*1024 + t)*4 + e%4: each wave
 // reads 1 KiB contiguous per dwordx4 load. Position p lives in thread
@@ -230,111 +251,196 @@ __device__ __forceinline__ uint32_t slot_pos(uint32_t e, uint32_t tid) {
 __device__ __forceinline__ uint32_t pos_owner(uint32_t p) { return (p >> 2) & (kBlock - 1); }
 __device__ __forceinline__ uint32_t pos_slot(uint32_t p) { return ((p >> 12) << 2) | (p & 3u); }
 
-template <int NCH, bool ALIGNED>
-__global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
-  // u16 history multiplicity per id (2 per word); reused as the
-  // general-path LDS when a row falls back.
-  __shared__ uint32_t s_cnt[kMaxFastV / 2];
+// Candidate order key: larger = earlier in the reference's sort (value desc,
+// then id asc).
+__device__ __forceinline__ uint64_t cand_order(uint32_t wkey, uint32_t id) {
+  return ((uint64_t)wkey << 32) | (uint64_t)(0xffffffffu - id);
+}
+
+// Threshold from a 12-bit key histogram of per-thread maxima (bins zeroed
+// beforehand, one atomic per thread already added): the lower edge of the
+// bin holding the Q-th largest maximum, lowered by the run of keys whose
+// v/T ties with it (lane l tests the key l+1 below; runs of ties are at most
+// ceil(2T)+1 long, so 64 covers T < 31). Two LDS barriers; every wave
+// computes the same result.
+__device__ __forceinline__ uint32_t hist_threshold(const uint32_t* s_bins, uint32_t* s_seg,
+                                                   uint32_t Q, float T, uint32_t wave,
+                                                   uint32_t lane) {
+  {
+    const uint4 q = reinterpret_cast<const uint4*>(s_bins)[kSelBins / 4 - 1u - (64u * wave + lane)];
+    const uint32_t tot = wave_incl_scan(q.x + q.y + q.z + q.w);
+    if (lane == 63) s_seg[wave] = tot;
+  }
+  lds_barrier();
+  const uint32_t sc = lane < kWaves ? s_seg[lane] : 0u;
+  const uint32_t si = wave_incl_scan(sc);
+  const uint64_t segm = __ballot(lane < kWaves && Q <= si);
+  const uint32_t seg = (uint32_t)__ffsll((unsigned long long)segm) - 1u;
+  const uint32_t kk = Q - (readlane_u32(si, seg) - readlane_u32(sc, seg));
+  const uint4 q = reinterpret_cast<const uint4*>(s_bins)[kSelBins / 4 - 1u - (64u * seg + lane)];
+  const uint32_t lt = q.x + q.y + q.z + q.w;  // descending within the lane: w, z, y, x
+  const uint32_t ci = wave_incl_scan(lt);
+  const uint64_t lm = __ballot(kk <= ci);
+  const uint32_t l = (uint32_t)__ffsll((unsigned long long)lm) - 1u;
+  const uint32_t need = kk - (readlane_u32(ci, l) - readlane_u32(lt, l));
+  const uint32_t cw = readlane_u32(q.w, l), cz = readlane_u32(q.z, l), cy = readlane_u32(q.y, l);
+  const uint32_t sub = need <= cw ? 0u : need <= cw + cz ? 1u : need <= cw + cz + cy ? 2u : 3u;
+  const uint32_t bin = kSelBins - 1u - (4u * (64u * seg + l) + sub);
+  const uint32_t tau = bin << (32 - kSelBits);
+  uint32_t lo = kKeyNaN;
+  if (tau > 0x007fffffu + 64u) {
+    const uint32_t wt = f2key(key2f(tau) / T);
+    const uint64_t ties = __ballot(f2key(key2f(tau - 1u - lane) / T) == wt);
+    const uint64_t run = ~ties;
+    if (run != 0ull) lo = tau - (uint32_t)(__ffsll((unsigned long long)run) - 1);
+  }
+  return lo > kKeyNaN ? lo : kKeyNaN;
+}
+
+// One row on the register path. Returns false (uniformly across the
+// workgroup, before writing any output) when the row needs the general
+// path; s_cnt is the u16 history multiplicity table (2 per word).
+template <int NCH, bool VEC>
+__device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
   __shared__ uint32_t s_pm[kBlock];      // per-thread mask of slots whose logit is penalized
   __shared__ uint32_t s_plist[kMaxPen];  // distinct penalized ids
-  __shared__ uint32_t s_hist[4 * 256];
-  __shared__ uint32_t s_ckey[kFastCand];
+  __shared__ __attribute__((aligned(16))) uint32_t s_bins[kSelBins];
+  __shared__ uint32_t s_seg[kWaves];
+  __shared__ uint32_t s_ckey[kFastCand];  // candidate v keys
   __shared__ uint32_t s_cid[kFastCand];
+  __shared__ __attribute__((aligned(16))) uint64_t s_ord[kFastCand];
   __shared__ uint32_t s_rank[kFastCand];
   __shared__ uint32_t s_skey[kMaxFastK];
   __shared__ uint32_t s_sid[kMaxFastK];
+  __shared__ __attribute__((aligned(16))) float s_tail[128];
   __shared__ float s_redv[kWaves];
   __shared__ uint32_t s_redi[kWaves];
   __shared__ uint32_t s_misc[8];
-  static_assert(sizeof(GenLds) <= sizeof(s_cnt), "general-path LDS must fit the count table");
   static_assert(NCH * 4 <= 32, "slot mask is 32 bits");
 
+  // The grid is exactly B workgroups.
   const uint32_t b = blockIdx.x;
-  if (b >= a.B) return;
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const llmhip_params P = load_params(a, b);
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
   const uint32_t V = a.V;
-  const uint32_t cls = row_class(P, V);
-  if (!(cls & a.row_class_mask)) return;
-  const float T = P.temperature, rp = P.repetition_penalty;
+  const bool hist_wave = wave < kHistWaves;
 
-  bool use_pen = P.repetition_penalty != 1.0f && a.hist && a.hist_offsets;
-  uint32_t h0 = 0, h1 = 0;
-  if (use_pen) {
-    h0 = a.hist_offsets[b];
-    h1 = a.hist_offsets[b + 1];
-    use_pen = h1 > h0;
-    if (use_pen && h1 - h0 >= 65536u) {
-      // A u16 count could overflow: take the general path.
-      general_row(a, b, P, *reinterpret_cast<GenLds*>(s_cnt));
-      return;
-    }
-  }
-  // History ids are loaded before the logits so the counting below only
-  // waits for them, not for the row.
-  uint32_t hid0 = 0xffffffffu, hid1 = 0xffffffffu;
-  if (use_pen) {
-    if (h0 + tid < h1) hid0 = a.hist[h0 + tid];
-    if (h0 + kBlock + tid < h1) hid1 = a.hist[h0 + kBlock + tid];
-  }
-
-  // All row loads in flight at once: NCH dwordx4 per lane.
+  // 1. Loads. Waves 0-3 first fetch the history ids (their address needs
+  //    the history offsets, one scalar round trip) and then their share of
+  //    the row; waves 4-15 put their share of the row in flight at once.
+  //    Row loads are branch-free: positions past V read position 0 and are
+  //    dropped below. Parameters and RNG state are scalar loads.
   const float* row = a.logits + (size_t)b * a.ld;
   float x[NCH * 4];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
+  auto load_chunk = [&](int c) __attribute__((always_inline)) {
     const uint32_t base = ((uint32_t)c * kBlock + tid) * 4u;
-    if (ALIGNED && base + 4u <= V) {
-      const float4 q = *reinterpret_cast<const float4*>(row + base);
+    if (VEC) {
+      const float4 q = *reinterpret_cast<const float4*>(row + (base < V ? base : 0u));
       x[4 * c + 0] = q.x;
       x[4 * c + 1] = q.y;
       x[4 * c + 2] = q.z;
       x[4 * c + 3] = q.w;
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[4 * c + j] = (base + j < V) ? row[base + j] : 0.0f;
+      for (int j = 0; j < 4; ++j) x[4 * c + j] = row[base + j < V ? base + j : 0u];
+    }
+  };
+  uint32_t h0 = 0, h1 = 0;
+  auto load_offsets = [&]() __attribute__((always_inline)) {
+    if (a.hist_offsets && a.hist) {
+      h0 = as_const(a.hist_offsets)[b];
+      h1 = as_const(a.hist_offsets)[b + 1];
+    }
+  };
+  uint32_t hid[kHistPerThread];
+#pragma unroll
+  for (uint32_t u = 0; u < kHistPerThread; ++u) hid[u] = 0xffffffffu;
+  if (hist_wave) {
+    load_offsets();
+    const uint32_t H0 = h1 > h0 ? h1 - h0 : 0u;
+#pragma unroll
+    for (uint32_t u = 0; u < kHistPerThread; ++u) {
+      const uint32_t j = tid + u * kHistWaves * 64u;
+      if (j < H0) hid[u] = a.hist[h0 + j];
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) load_chunk(c);
+  __builtin_amdgcn_sched_barrier(0);
+  if (!hist_wave) load_offsets();
 
-  if (use_pen) {
-    for (uint32_t i = tid; i < (V + 1) / 2; i += kBlock) s_cnt[i] = 0u;
+  const llmhip_params P = load_params(a, b);
+  const uint64_t rng0 = as_const(a.rng_state)[b];
+  {
+    uint4* c4 = reinterpret_cast<uint4*>(s_cnt);
+    for (uint32_t i = tid; i < (V + 7) / 8; i += kBlock) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+    reinterpret_cast<uint4*>(s_bins)[tid] = make_uint4(0u, 0u, 0u, 0u);  // kSelBins / 4 == kBlock
     s_pm[tid] = 0u;
+    for (uint32_t i = tid; i < kFastCand; i += kBlock) s_rank[i] = 0u;
+    if (tid < 8) s_misc[tid] = 0u;
   }
-  s_hist[tid] = 0u;  // 4 x 256 bins == kBlock
-  if (tid < 8) s_misc[tid] = 0u;
+  const uint32_t cls = row_class(P, V);
+  if (!(cls & a.row_class_mask)) return true;
+  const float T = P.temperature, rp = P.repetition_penalty;
+  const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
+  if (H >= 65536u) {
+    // A u16 count could overflow: take the general path.
+    return false;
+  }
+  const bool use_pen = H > 0;
   lds_barrier();
 
-  // History multiplicities (integer LDS atomics: the counts do not depend
-  // on the order). The first occurrence of an id enlists it for one
-  // processor lane and marks its slot in the owner's mask.
-  uint32_t D = 0;
-  if (use_pen) {
-    auto add_hist = [&](uint32_t id) {
-      if (id < V) {
-        const uint32_t sh = (id & 1u) << 4;
-        const uint32_t old = atomicAdd(&s_cnt[id >> 1], 1u << sh);
-        if (((old >> sh) & 0xffffu) == 0u) {
-          const uint32_t q = atomicAdd(&s_misc[3], 1u);
-          if (q < kMaxPen) s_plist[q] = id;
-          atomicOr(&s_pm[pos_owner(id)], 1u << pos_slot(id));
-        }
+  // 2. History multiplicities (integer LDS atomics: the counts do not
+  //    depend on the order), counted by waves 0-3 while the row streams in.
+  //    The first occurrence of an id enlists it for one processor lane and
+  //    marks its slot in the owner thread's mask.
+  auto add_hist = [&](uint32_t id) __attribute__((always_inline)) {
+    if (id < V) {
+      const uint32_t sh = (id & 1u) << 4;
+      const uint32_t old = atomicAdd(&s_cnt[id >> 1], 1u << sh);
+      if (((old >> sh) & 0xffffu) == 0u) {
+        const uint32_t q = atomicAdd(&s_misc[3], 1u);
+        if (q < kMaxPen) s_plist[q] = id;
+        atomicOr(&s_pm[pos_owner(id)], 1u << pos_slot(id));
       }
-    };
-    add_hist(hid0);
-    add_hist(hid1);
-    for (uint32_t j = h0 + 2u * kBlock + tid; j < h1; j += kBlock) add_hist(a.hist[j]);
-    lds_barrier();
-    D = s_misc[3];
-    if (D > kMaxPen) {
-      __syncthreads();
-      general_row(a, b, P, *reinterpret_cast<GenLds*>(s_cnt));
-      return;
     }
+  };
+  if (use_pen && hist_wave) {
+#pragma unroll
+    for (uint32_t u = 0; u < kHistPerThread; ++u) add_hist(hid[u]);
+    for (uint32_t j = tid + kHistPerThread * kHistWaves * 64u; j < H; j += kHistWaves * 64u)
+      add_hist(a.hist[h0 + j]);
   }
 
-  // Processor lanes: each distinct penalized id is gathered once (its line
-  // is being streamed by the row loads, so this merges in L2) and given
-  // mask -> penalty (m times in sequence: no float atomics) here.
+  // 3. Speculative threshold from the first quarter of the row (it arrives
+  //    first): per-thread maxima over chunks 0..S-1 go into the key
+  //    histogram while the rest of the row is still in flight. It is
+  //    checked against the full row in 6.
+  constexpr int S = NCH >= 4 ? NCH / 4 : NCH;
+  const uint32_t K = P.top_k;  // 0 < K < V, K <= 1024 (row class)
+  const bool greedy = cls == kClassGreedy;
+  auto chunk_full = [&](int c) __attribute__((always_inline)) { return (uint32_t)(c + 1) * 4u * kBlock <= V; };
+  if (!greedy) {
+    float sm = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < S; ++c) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v = x[4 * c + j];
+        sm = (chunk_full(c) || slot_pos(4 * c + j, tid) < V) ? fmaxf(sm, v) : sm;
+      }
+    }
+    const uint32_t sk = slot_pos(0, tid) < V ? f2key(sm) : kKeyNone;
+    atomicAdd(&s_bins[sk >> (32 - kSelBits)], 1u);
+  }
+  lds_barrier();
+  const uint32_t D = use_pen ? s_misc[3] : 0u;
+  if (D > kMaxPen) return false;
+
+  // 4. Processor lanes: each distinct penalized id is gathered once (its
+  //    line is being streamed by the row loads, so this merges in L2) and
+  //    gets mask -> penalty (m times in sequence: no float atomics) here.
   float gv[kPenPerThread];
   uint32_t gp[kPenPerThread], gm[kPenPerThread];
 #pragma unroll
@@ -352,7 +458,7 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   }
   const uint32_t pm = use_pen ? s_pm[tid] : 0u;
 
-  if (cls == kClassGreedy) {
+  if (greedy) {
     // ops/loss.rs:6-16 over the penalized, masked row (before temperature).
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
@@ -380,180 +486,150 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
       a.out_ids[b] = w == 0xffffffffu ? 0u : w;
       if (a.out_kept) a.out_kept[b] = 0u;
     }
-    return;
+    return true;
   }
 
-  // Keys of the pre-temperature values v (mask applied; penalized logits
-  // are represented by their processor lane instead). Dividing by T > 0
-  // is monotone, so the top-k by v contains the top-k by v/T except for
-  // values that the division merges into ties; those are caught below.
-  uint32_t key[NCH * 4];
-  uint32_t tmax = kKeyNone;
-#pragma unroll
-  for (int e = 0; e < NCH * 4; ++e) {
-    const uint32_t pos = slot_pos(e, tid);
-    float v = x[e];
-    if (a.allowed && masked_out(a, pos)) v = -INFINITY;
-    uint32_t k = f2key(v);
-    if (pos >= V || ((pm >> e) & 1u)) k = kKeyNone;
-    key[e] = k;
-    tmax = k > tmax ? k : tmax;
+  // Speculative threshold: aim at ~1.6 K candidates over the full row. A
+  // threshold at or below -inf (fewer than K finite logits in reach) goes to
+  // the general path.
+  uint32_t thr;
+  {
+    const uint32_t Q = S == NCH ? K : (uint32_t)((8u * K * S + 5u * NCH - 1u) / (5u * NCH)) + 2u;
+    thr = hist_threshold(s_bins, s_seg, Q, T, wave, lane);
   }
-  uint32_t gk[kPenPerThread];
+  if (thr <= 0x007fffffu) return false;
+
+  // 5. Pre-temperature values v: mask applied, penalized slots turned into
+  //    NaN (their processor lane stands in for them; NaN is never >= the
+  //    threshold and fmaxf ignores it), padding turned into NaN.
+  if (a.allowed) {
+#pragma unroll
+    for (int e = 0; e < NCH * 4; ++e)
+      if (masked_out(a, slot_pos(e, tid))) x[e] = -INFINITY;
+  }
+  if (use_pen) {
+#pragma unroll
+    for (int e = 0; e < NCH * 4; ++e) {
+      const uint32_t t = (uint32_t)((int32_t)(pm << (31 - e)) >> 31);
+      x[e] = __uint_as_float((t & 0x7fc00000u) | (~t & __float_as_uint(x[e])));
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (!chunk_full(c)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (slot_pos(4 * c + j, tid) >= V) x[4 * c + j] = __uint_as_float(0x7fc00000u);
+    }
+  }
+  float gx[kPenPerThread];  // penalized values of this thread's processor ids (NaN = none)
 #pragma unroll
   for (uint32_t r = 0; r < kPenPerThread; ++r) {
-    gk[r] = kKeyNone;
+    gx[r] = __uint_as_float(0x7fc00000u);
     if (gp[r] != 0xffffffffu) {
       float v = gv[r];
       if (masked_out(a, gp[r])) v = -INFINITY;
-      gk[r] = f2key(apply_penalty(v, gm[r], rp));
-      tmax = gk[r] > tmax ? gk[r] : tmax;
+      gx[r] = apply_penalty(v, gm[r], rp);
     }
   }
 
-  // tau = exact K-th largest of the 1024 per-thread maxima (4 x 8-bit LDS
-  // radix passes, bins scanned from the top by wave 0). At least K
-  // elements have key >= tau and they live in at most K threads.
-  const uint32_t K = P.top_k;  // 0 < K < V, K <= 1024 (row class)
-  uint32_t prefix = 0u, kk = K;
+  // 6. Candidates: v >= thr (the division by T > 0 is monotone, so the
+  //    top-k by v/T lies among them once there are at least K, the
+  //    threshold having been lowered by the values the division merges into
+  //    ties with it). One LDS atomic per wave; keys only for candidates.
+  //    The count proves the threshold: K <= n <= capacity. Otherwise the
+  //    exact threshold from all 1024 per-thread maxima is used.
+  auto append = [&](uint32_t th, uint32_t counter) __attribute__((always_inline)) {
+    const float tf = key2f(th);
+    uint32_t mine = 0u;
 #pragma unroll
-  for (uint32_t pass = 0; pass < 4; ++pass) {
-    const uint32_t shift = 24u - 8u * pass;
-    const uint32_t hi_mask = pass == 0 ? 0u : (0xffffffffu << (shift + 8u));
-    if ((tmax & hi_mask) == prefix) atomicAdd(&s_hist[pass * 256u + ((tmax >> shift) & 255u)], 1u);
-    lds_barrier();
-    if (wave == 0) {
-      const uint32_t d0 = 255u - 4u * lane;
-      const uint32_t* h = s_hist + pass * 256u;
-      const uint32_t c0 = h[d0], c1 = h[d0 - 1], c2 = h[d0 - 2], c3 = h[d0 - 3];
-      const uint32_t tot = c0 + c1 + c2 + c3;
-      const uint32_t incl = wave_incl_scan(tot);
-      uint32_t cum = incl - tot;
-      uint32_t np = 0u, nk = 0u;
-      const bool mine = cum < kk && kk <= incl;
-      if (mine) {
-        uint32_t d;
-        if (cum + c0 >= kk) {
-          d = d0;
-        } else if (cum += c0, cum + c1 >= kk) {
-          d = d0 - 1;
-        } else if (cum += c1, cum + c2 >= kk) {
-          d = d0 - 2;
-        } else {
-          cum += c2;
-          d = d0 - 3;
-        }
-        np = prefix | (d << shift);
-        nk = kk - cum;
-      }
-      const uint64_t who = __ballot(mine);
-      const uint32_t src = who ? (uint32_t)__ffsll((unsigned long long)who) - 1u : 0u;
-      np = readlane_u32(np, src);
-      nk = readlane_u32(nk, src);
-      if (pass < 3) {
-        if (lane == 0) {
-          s_misc[0] = np;
-          s_misc[1] = nk;
-        }
-      } else {
-        // Lowest v key whose v/T equals (tau)/T: the candidate threshold.
-        // Lane l tests the value l+1 keys below tau; the run of ties from
-        // the top is at most ceil(2T)+1 long, so one wave covers T < 31.
-        uint32_t lo = np;
-        if (np > kKeyNaN + 64u) {
-          const uint32_t wt = f2key(key2f(np) / T);
-          const bool tie = f2key(key2f(np - 1u - lane) / T) == wt;
-          const uint64_t ties = __ballot(tie);
-          const uint64_t run = ~ties;
-          if (run == 0ull) {
-            lo = kKeyNaN;  // more than 64 tied values: take everything
-          } else {
-            lo = np - (uint32_t)(__ffsll((unsigned long long)run) - 1);
+    for (int e = 0; e < NCH * 4; ++e) mine += x[e] >= tf ? 1u : 0u;
+#pragma unroll
+    for (uint32_t r = 0; r < kPenPerThread; ++r) mine += gx[r] >= tf ? 1u : 0u;
+    const uint32_t incl = wave_incl_scan(mine);
+    const uint32_t wtot = readlane_u32(incl, 63);
+    uint32_t wbase = 0u;
+    if (lane == 0 && wtot) wbase = atomicAdd(&s_misc[counter], wtot);
+    wbase = readlane_u32(wbase, 0);
+    if (wtot) {
+      uint32_t slot = wbase + incl - mine;
+#pragma unroll
+      for (int e = 0; e < NCH * 4; ++e) {
+        if (x[e] >= tf) {
+          if (slot < kFastCand) {
+            s_ckey[slot] = f2key(x[e]);
+            s_cid[slot] = slot_pos(e, tid);
           }
-        } else {
-          lo = kKeyNaN;
-        }
-        if (lane == 0) {
-          s_misc[0] = np;
-          s_misc[1] = lo;
+          ++slot;
         }
       }
-    }
-    lds_barrier();
-    prefix = s_misc[0];
-    kk = s_misc[1];
-  }
-  // After the last pass s_misc[1] holds the threshold.
-  const uint32_t thr = kk > kKeyNaN ? kk : kKeyNaN;
-
-  // Append candidates (key >= thr) with their post-temperature key: one
-  // LDS atomic per wave, one division per candidate.
-  uint32_t mine = 0u;
 #pragma unroll
-  for (int e = 0; e < NCH * 4; ++e) mine += key[e] >= thr ? 1u : 0u;
-#pragma unroll
-  for (uint32_t r = 0; r < kPenPerThread; ++r) mine += gk[r] >= thr ? 1u : 0u;
-  const uint32_t incl = wave_incl_scan(mine);
-  const uint32_t wtot = readlane_u32(incl, 63);
-  uint32_t wbase = 0u;
-  if (lane == 0 && wtot) wbase = atomicAdd(&s_misc[2], wtot);
-  wbase = readlane_u32(wbase, 0);
-  uint32_t slot = wbase + incl - mine;
-#pragma unroll
-  for (int e = 0; e < NCH * 4; ++e) {
-    if (key[e] >= thr) {
-      if (slot < kFastCand) {
-        s_ckey[slot] = f2key(key2f(key[e]) / T);
-        s_cid[slot] = slot_pos(e, tid);
+      for (uint32_t r = 0; r < kPenPerThread; ++r) {
+        if (gx[r] >= tf) {
+          if (slot < kFastCand) {
+            s_ckey[slot] = f2key(gx[r]);
+            s_cid[slot] = gp[r];
+          }
+          ++slot;
+        }
       }
-      ++slot;
     }
-  }
-#pragma unroll
-  for (uint32_t r = 0; r < kPenPerThread; ++r) {
-    if (gk[r] >= thr) {
-      if (slot < kFastCand) {
-        s_ckey[slot] = f2key(key2f(gk[r]) / T);
-        s_cid[slot] = gp[r];
-      }
-      ++slot;
-    }
-  }
+  };
+  append(thr, 2);
   lds_barrier();
-  const uint32_t n = s_misc[2];
-  if (n > kFastCand) {
-    // Heavy ties at the threshold: not bounded by the register path.
-    __syncthreads();
-    general_row(a, b, P, *reinterpret_cast<GenLds*>(s_cnt));
-    return;
+  uint32_t n = s_misc[2];
+  if (n < K || n > kFastCand) {
+    // The count table is dead by now: it holds the exact histogram.
+    uint32_t* bins2 = s_cnt;
+    reinterpret_cast<uint4*>(bins2)[tid] = make_uint4(0u, 0u, 0u, 0u);
+    float tm = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < NCH * 4; ++e) tm = fmaxf(tm, x[e]);
+#pragma unroll
+    for (uint32_t r = 0; r < kPenPerThread; ++r) tm = fmaxf(tm, gx[r]);
+    lds_barrier();
+    atomicAdd(&bins2[(tm == tm ? f2key(tm) : kKeyNone) >> (32 - kSelBits)], 1u);
+    lds_barrier();
+    thr = hist_threshold(bins2, s_seg, K, T, wave, lane);
+    if (thr <= 0x007fffffu) return false;
+    append(thr, 6);
+    lds_barrier();
+    n = s_misc[6];
+    // Heavy ties or an unusually flat top: not bounded by the register
+    // path.
+    if (n > kFastCand) return false;
   }
 
-  // Rank by (w key desc, id asc): rank(i) = #{j : cand j precedes cand i},
-  // the j range split over all waves.
-  for (uint32_t i = tid; i < n; i += kBlock) s_rank[i] = 0u;
+  // 7. Post-temperature order keys, one division per candidate
+  //    (generate.rs:357-359), then ranks rank(i) = #{j : ord_j > ord_i},
+  //    the j range split over all waves.
+  for (uint32_t i = tid; i < n; i += kBlock) s_ord[i] = cand_order(f2key(key2f(s_ckey[i]) / T), s_cid[i]);
   lds_barrier();
   if (n <= kBlock) {
     const uint32_t n64 = (n + 63u) & ~63u;
-    const uint32_t groups = n64 ? kBlock / n64 : 1u;
-    const uint32_t i = n64 ? tid % n64 : 0u, g = n64 ? tid / n64 : 0u;
+    const uint32_t groups = kBlock / n64;
+    const uint32_t i = tid % n64, g = tid / n64;
     if (g < groups && i < n) {
-      const uint32_t ki = s_ckey[i], ii = s_cid[i];
-      const uint32_t j0 = n * g / groups, j1 = n * (g + 1) / groups;
-      uint32_t r = 0u;
-      for (uint32_t j = j0; j < j1; ++j) {
-        const uint32_t kj = s_ckey[j], ij = s_cid[j];
-        r += (kj > ki || (kj == ki && ij < ii)) ? 1u : 0u;
+      const uint64_t oi = s_ord[i];
+      const uint32_t j0 = (n * g / groups) & ~1u;
+      const uint32_t j1 = g + 1 == groups ? n : ((n * (g + 1) / groups) & ~1u);
+      uint32_t r = 0u, j = j0;
+      for (; j + 8 <= j1; j += 8) {
+        const ulonglong2 p0 = *reinterpret_cast<const ulonglong2*>(&s_ord[j]);
+        const ulonglong2 p1 = *reinterpret_cast<const ulonglong2*>(&s_ord[j + 2]);
+        const ulonglong2 p2 = *reinterpret_cast<const ulonglong2*>(&s_ord[j + 4]);
+        const ulonglong2 p3 = *reinterpret_cast<const ulonglong2*>(&s_ord[j + 6]);
+        r += (p0.x > oi) + (p0.y > oi) + (p1.x > oi) + (p1.y > oi) + (p2.x > oi) + (p2.y > oi) +
+             (p3.x > oi) + (p3.y > oi);
       }
+      for (; j < j1; ++j) r += s_ord[j] > oi ? 1u : 0u;
       atomicAdd(&s_rank[i], r);
     }
   } else {
     for (uint32_t i = tid; i < n; i += kBlock) {
-      const uint32_t ki = s_ckey[i], ii = s_cid[i];
+      const uint64_t oi = s_ord[i];
       uint32_t r = 0u;
-      for (uint32_t j = 0; j < n; ++j) {
-        const uint32_t kj = s_ckey[j], ij = s_cid[j];
-        r += (kj > ki || (kj == ki && ij < ii)) ? 1u : 0u;
-      }
+      for (uint32_t j = 0; j < n; ++j) r += s_ord[j] > oi ? 1u : 0u;
       s_rank[i] = r;
     }
   }
@@ -561,13 +637,34 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   for (uint32_t i = tid; i < n; i += kBlock) {
     const uint32_t r = s_rank[i];
     if (r < K) {
-      s_skey[r] = s_ckey[i];
-      s_sid[r] = s_cid[i];
+      const uint64_t o = s_ord[i];
+      s_skey[r] = (uint32_t)(o >> 32);
+      s_sid[r] = 0xffffffffu - (uint32_t)o;
     }
   }
   lds_barrier();
+
+  // 8. The sequential tail (one wave).
   if (wave == 0) {
-    draw_tail(a, b, P, K, [&](uint32_t i) { return s_skey[i]; }, [&](uint32_t i) { return s_sid[i]; });
+    if (K <= 64) {
+      draw_tail_small(a, b, P, K, lane < K ? s_skey[lane] : kKeyNone, lane < K ? s_sid[lane] : 0u,
+                      rng0, s_tail);
+    } else {
+      draw_tail(a, b, P, K, [&](uint32_t i) { return s_skey[i]; }, [&](uint32_t i) { return s_sid[i]; });
+    }
+  }
+  return true;
+}
+
+template <int NCH, bool VEC>
+__global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
+  // u16 history multiplicities; also the general path's LDS when a row
+  // falls back.
+  __shared__ __attribute__((aligned(16))) uint32_t s_cnt[kMaxFastV / 2];
+  static_assert(sizeof(GenLds) <= sizeof(s_cnt), "general-path LDS must fit the count table");
+  if (!fast_row<NCH, VEC>(a, s_cnt)) {
+    __syncthreads();
+    general_row(a, blockIdx.x, *reinterpret_cast<GenLds*>(s_cnt));
   }
 }
 
@@ -575,8 +672,8 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
 // Host-side launch.
 // ---------------------------------------------------------------------------
 template <int NCH>
-static hipError_t launch_fast_nch(const SampleArgs& a, bool aligned, hipStream_t s) {
-  if (aligned) {
+static hipError_t launch_fast_nch(const SampleArgs& a, bool vec, hipStream_t s) {
+  if (vec) {
     hipLaunchKernelGGL((sample_fast_kernel<NCH, true>), dim3(a.B), dim3(kBlock), 0, s, a);
   } else {
     hipLaunchKernelGGL((sample_fast_kernel<NCH, false>), dim3(a.B), dim3(kBlock), 0, s, a);
@@ -584,11 +681,11 @@ static hipError_t launch_fast_nch(const SampleArgs& a, bool aligned, hipStream_t
   return hipGetLastError();
 }
 
-hipError_t launch_fast(const SampleArgs& a, bool aligned, hipStream_t s) {
-  if (a.V <= 4096) return launch_fast_nch<1>(a, aligned, s);
-  if (a.V <= 8192) return launch_fast_nch<2>(a, aligned, s);
-  if (a.V <= 16384) return launch_fast_nch<4>(a, aligned, s);
-  return launch_fast_nch<8>(a, aligned, s);
+hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s) {
+  if (a.V <= 4096) return launch_fast_nch<1>(a, vec, s);
+  if (a.V <= 8192) return launch_fast_nch<2>(a, vec, s);
+  if (a.V <= 16384) return launch_fast_nch<4>(a, vec, s);
+  return launch_fast_nch<8>(a, vec, s);
 }
 
 hipError_t launch_general(const SampleArgs& a, hipStream_t s) {

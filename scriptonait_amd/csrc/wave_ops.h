@@ -7,14 +7,22 @@ namespace llmhip {
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// DPP move: lanes whose source is outside the pattern (or rows outside
+// ROW_MASK) read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp0(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP: row_shr 1,2,4,8
+// within each row of 16, then row_bcast:15 and row_bcast:31 across rows.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (uint32_t off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+  x += dpp0<0x111>(x);
+  x += dpp0<0x112>(x);
+  x += dpp0<0x114>(x);
+  x += dpp0<0x118>(x);
+  x += dpp0<0x142, 0xa>(x);
+  x += dpp0<0x143, 0xc>(x);
   return x;
 }
 
