@@ -45,7 +45,24 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of benchmarking, run 10 device-to-device copies of MIB MiB "
+                         "(a plain copy kernel of known size, to scale rocprofv3 byte counters)")
     return ap.parse_args()
+
+
+def calibrate_copy(mib: int) -> None:
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes_read": n, "calibrate_copy_bytes_written": n,
+                      "copies": 10}), flush=True)
 
 
 def cpu_baseline(w, seconds: float) -> dict:
@@ -86,6 +103,10 @@ def main():
               "throughput at N GPUs is N times the one-GPU figure by construction.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     import torch
 
