@@ -146,12 +146,16 @@ __device__ __forceinline__ void draw_tail_small(const SampleArgs& a, uint32_t b,
     float4 v[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = b4[q];
+    bool go = true;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      sum += v[q].x;
-      sum += v[q].y;
-      sum += v[q].z;
-      sum += v[q].w;
+      if (go) {
+        sum += v[q].x;
+        sum += v[q].y;
+        sum += v[q].z;
+        sum += v[q].w;
+        if ((q & 1) && 4u * (q + 1) >= n) go = false;
+      }
     }
   }
   // generate.rs:375-377
@@ -180,19 +184,27 @@ __device__ __forceinline__ void draw_tail_small(const SampleArgs& a, uint32_t b,
 #pragma unroll
   for (int q = 0; q < 16; ++q) pv[q] = b4[q];
   {
+    // Stops after the block of 8 where the fold reaches top_p (every lane
+    // holds the same running value, so the exit is uniform).
+    const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
     float c = 0.0f;
+    bool go = true;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      float4 o;
-      c += pv[q].x;
-      o.x = c;
-      c += pv[q].y;
-      o.y = c;
-      c += pv[q].z;
-      o.z = c;
-      c += pv[q].w;
-      o.w = c;
-      if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
+      if (go) {
+        float4 o;
+        c += pv[q].x;
+        o.x = c;
+        c += pv[q].y;
+        o.y = c;
+        c += pv[q].z;
+        o.z = c;
+        c += pv[q].w;
+        o.w = c;
+        if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
+        // c is the same in every lane: read it as a scalar.
+        if ((q & 1) && (4u * (q + 1) >= keep || __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(c))) >= tp)) go = false;
+      }
     }
   }
   const float my_c = lane < keep ? cbuf[lane] : 0.0f;
@@ -206,19 +218,25 @@ __device__ __forceinline__ void draw_tail_small(const SampleArgs& a, uint32_t b,
   // generate.rs:412-419: r_i = r before subtracting p_i; lane i tests r_i < p_i.
   const float ur = next_f32(st);
   {
+    // r - p < 0 exactly when r < p, so r turns negative at the pick: stop
+    // after that block of 8.
     float r = ur * total;
+    bool go = true;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      float4 o;
-      o.x = r;
-      r -= pv[q].x;
-      o.y = r;
-      r -= pv[q].y;
-      o.z = r;
-      r -= pv[q].z;
-      o.w = r;
-      r -= pv[q].w;
-      if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
+      if (go) {
+        float4 o;
+        o.x = r;
+        r -= pv[q].x;
+        o.y = r;
+        r -= pv[q].y;
+        o.z = r;
+        r -= pv[q].z;
+        o.w = r;
+        r -= pv[q].w;
+        if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
+        if ((q & 1) && (4u * (q + 1) >= stop || __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(r))) < 0.0f)) go = false;
+      }
     }
   }
   const float my_r = lane < stop ? cbuf[lane] : 0.0f;

@@ -241,6 +241,7 @@ constexpr uint32_t kSelBits = 12;     // threshold histogram: top 12 key bits
 constexpr uint32_t kSelBins = 1u << kSelBits;
 constexpr uint32_t kHistWaves = 4;    // waves that load and count the history
 constexpr uint32_t kHistPerThread = 4;
+constexpr uint32_t kWaveCand = kFastCand / kWaves;  // per-wave candidate region
 
 // Element e of thread t holds position ((e/4)*1024 + t)*4 + e%4: each wave
 // reads 1 KiB contiguous per dwordx4 load. Position p lives in thread
@@ -306,10 +307,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
   __shared__ uint32_t s_plist[kMaxPen];  // distinct penalized ids
   __shared__ __attribute__((aligned(16))) uint32_t s_bins[kSelBins];
   __shared__ uint32_t s_seg[kWaves];
-  __shared__ uint32_t s_ckey[kFastCand];  // candidate v keys
-  __shared__ uint32_t s_cid[kFastCand];
-  __shared__ __attribute__((aligned(16))) uint64_t s_ord[kFastCand];
-  __shared__ uint32_t s_rank[kFastCand];
+  __shared__ uint32_t s_wkey[kWaves * kWaveCand];  // per-wave candidate regions: v key
+  __shared__ uint32_t s_wid[kWaves * kWaveCand];   //                              id
+  __shared__ __attribute__((aligned(16))) uint64_t s_ord[kFastCand];  // compacted order keys
   __shared__ uint32_t s_skey[kMaxFastK];
   __shared__ uint32_t s_sid[kMaxFastK];
   __shared__ __attribute__((aligned(16))) float s_tail[128];
@@ -377,17 +377,14 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
     for (uint32_t i = tid; i < (V + 7) / 8; i += kBlock) c4[i] = make_uint4(0u, 0u, 0u, 0u);
     reinterpret_cast<uint4*>(s_bins)[tid] = make_uint4(0u, 0u, 0u, 0u);  // kSelBins / 4 == kBlock
     s_pm[tid] = 0u;
-    for (uint32_t i = tid; i < kFastCand; i += kBlock) s_rank[i] = 0u;
     if (tid < 8) s_misc[tid] = 0u;
   }
   const uint32_t cls = row_class(P, V);
   if (!(cls & a.row_class_mask)) return true;
   const float T = P.temperature, rp = P.repetition_penalty;
   const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
-  if (H >= 65536u) {
-    // A u16 count could overflow: take the general path.
-    return false;
-  }
+  // A u16 count could overflow: take the general path.
+  if (H >= 65536u) return false;
   const bool use_pen = H > 0;
   lds_barrier();
 
@@ -415,8 +412,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
 
   // 3. Speculative threshold from the first quarter of the row (it arrives
   //    first): per-thread maxima over chunks 0..S-1 go into the key
-  //    histogram while the rest of the row is still in flight. It is
-  //    checked against the full row in 6.
+  //    histogram while the rest of the row is still in flight. The count in
+  //    6 proves or rejects it.
   constexpr int S = NCH >= 4 ? NCH / 4 : NCH;
   const uint32_t K = P.top_k;  // 0 < K < V, K <= 1024 (row class)
   const bool greedy = cls == kClassGreedy;
@@ -457,6 +454,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
     }
   }
   const uint32_t pm = use_pen ? s_pm[tid] : 0u;
+  // Logit v as the sampler sees it before temperature (mask applied) for a
+  // slot this thread owns; penalized slots are handled by processor lanes.
+  auto slot_ok = [&](int e) __attribute__((always_inline)) {
+    const uint32_t pos = slot_pos(e, tid);
+    return (chunk_full(e >> 2) || pos < V) && !((pm >> e) & 1u) && !(a.allowed && masked_out(a, pos));
+  };
 
   if (greedy) {
     // ops/loss.rs:6-16 over the penalized, masked row (before temperature).
@@ -464,14 +467,14 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
     uint32_t bi = 0xffffffffu;
 #pragma unroll
     for (int e = 0; e < NCH * 4; ++e) {
-      const uint32_t pos = slot_pos(e, tid);
-      float v = x[e];
-      if (a.allowed && masked_out(a, pos)) v = -INFINITY;
-      if (pos < V && !((pm >> e) & 1u) && v > bv) {
+      const float v = x[e];
+      if (v > bv && slot_ok(e)) {
         bv = v;
-        bi = pos;
+        bi = slot_pos(e, tid);
       }
     }
+    // A masked slot is -inf, which never beats anything; a masked-out slot
+    // skipped above is therefore equivalent.
 #pragma unroll
     for (uint32_t r = 0; r < kPenPerThread; ++r) {
       if (gp[r] != 0xffffffffu) {
@@ -488,10 +491,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
     }
     return true;
   }
-
-  // Speculative threshold: aim at ~1.6 K candidates over the full row. A
-  // threshold at or below -inf (fewer than K finite logits in reach) goes to
-  // the general path.
+  // 5. Speculative threshold: aim at ~1.6 K candidates over the full row.
+  //    A threshold at or below -inf (fewer than K finite logits in reach)
+  //    goes to the general path.
   uint32_t thr;
   {
     const uint32_t Q = S == NCH ? K : (uint32_t)((8u * K * S + 5u * NCH - 1u) / (5u * NCH)) + 2u;
@@ -499,147 +501,163 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, uint32_t* s_cnt) {
   }
   if (thr <= 0x007fffffu) return false;
 
-  // 5. Pre-temperature values v: mask applied, penalized slots turned into
-  //    NaN (their processor lane stands in for them; NaN is never >= the
-  //    threshold and fmaxf ignores it), padding turned into NaN.
-  if (a.allowed) {
-#pragma unroll
-    for (int e = 0; e < NCH * 4; ++e)
-      if (masked_out(a, slot_pos(e, tid))) x[e] = -INFINITY;
-  }
-  if (use_pen) {
+  // 6. Candidates: v >= thr. Dividing by T > 0 is monotone, so the top-k by
+  //    v/T lies among them once there are at least K (the threshold was
+  //    lowered by the values the division merges into ties with it). The
+  //    scan is one compare per logit; the rare hits go to this wave's own
+  //    LDS region through a ballot, so no cross-wave offsets are needed.
+  //    Each wave then turns its hits into post-temperature order keys (one
+  //    division per hit, generate.rs:357-359) and appends them to the
+  //    compact list with one LDS atomic.
+  // Hits go to this wave's region as (raw value bits, position): one compare
+  // per logit, and for the rare slots where some lane hits, a ballot offset
+  // and two LDS writes. Validity (penalized slot, padding, mask) and keys
+  // are settled per hit afterwards, one lane per hit.
+  auto scan_own = [&](float tf, uint32_t& cnt) __attribute__((always_inline)) {
+    uint32_t* rk = s_wkey + wave * kWaveCand;
+    uint32_t* ri = s_wid + wave * kWaveCand;
 #pragma unroll
     for (int e = 0; e < NCH * 4; ++e) {
-      const uint32_t t = (uint32_t)((int32_t)(pm << (31 - e)) >> 31);
-      x[e] = __uint_as_float((t & 0x7fc00000u) | (~t & __float_as_uint(x[e])));
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    if (!chunk_full(c)) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (slot_pos(4 * c + j, tid) >= V) x[4 * c + j] = __uint_as_float(0x7fc00000u);
-    }
-  }
-  float gx[kPenPerThread];  // penalized values of this thread's processor ids (NaN = none)
-#pragma unroll
-  for (uint32_t r = 0; r < kPenPerThread; ++r) {
-    gx[r] = __uint_as_float(0x7fc00000u);
-    if (gp[r] != 0xffffffffu) {
-      float v = gv[r];
-      if (masked_out(a, gp[r])) v = -INFINITY;
-      gx[r] = apply_penalty(v, gm[r], rp);
-    }
-  }
-
-  // 6. Candidates: v >= thr (the division by T > 0 is monotone, so the
-  //    top-k by v/T lies among them once there are at least K, the
-  //    threshold having been lowered by the values the division merges into
-  //    ties with it). One LDS atomic per wave; keys only for candidates.
-  //    The count proves the threshold: K <= n <= capacity. Otherwise the
-  //    exact threshold from all 1024 per-thread maxima is used.
-  auto append = [&](uint32_t th, uint32_t counter) __attribute__((always_inline)) {
-    const float tf = key2f(th);
-    uint32_t mine = 0u;
-#pragma unroll
-    for (int e = 0; e < NCH * 4; ++e) mine += x[e] >= tf ? 1u : 0u;
-#pragma unroll
-    for (uint32_t r = 0; r < kPenPerThread; ++r) mine += gx[r] >= tf ? 1u : 0u;
-    const uint32_t incl = wave_incl_scan(mine);
-    const uint32_t wtot = readlane_u32(incl, 63);
-    uint32_t wbase = 0u;
-    if (lane == 0 && wtot) wbase = atomicAdd(&s_misc[counter], wtot);
-    wbase = readlane_u32(wbase, 0);
-    if (wtot) {
-      uint32_t slot = wbase + incl - mine;
-#pragma unroll
-      for (int e = 0; e < NCH * 4; ++e) {
-        if (x[e] >= tf) {
-          if (slot < kFastCand) {
-            s_ckey[slot] = f2key(x[e]);
-            s_cid[slot] = slot_pos(e, tid);
-          }
-          ++slot;
+      const bool hit = x[e] >= tf;
+      const uint64_t m = __ballot(hit);
+      if (m) {
+        const uint32_t o = cnt + lanes_below(m);
+        if (hit && o < kWaveCand) {
+          rk[o] = __float_as_uint(x[e]);
+          ri[o] = slot_pos(e, tid) | ((uint32_t)e << 24);
         }
-      }
-#pragma unroll
-      for (uint32_t r = 0; r < kPenPerThread; ++r) {
-        if (gx[r] >= tf) {
-          if (slot < kFastCand) {
-            s_ckey[slot] = f2key(gx[r]);
-            s_cid[slot] = gp[r];
-          }
-          ++slot;
-        }
+        cnt += (uint32_t)__popcll((unsigned long long)m);
       }
     }
   };
-  append(thr, 2);
+  // Processor values (they wait for the gathers, which complete after the
+  // row): mask -> penalty m times in sequence.
+  float gx[kPenPerThread];  // NaN = none
+  auto finish_processors = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t r = 0; r < kPenPerThread; ++r) {
+      gx[r] = __uint_as_float(0x7fc00000u);
+      if (gp[r] != 0xffffffffu) {
+        float v = gv[r];
+        if (masked_out(a, gp[r])) v = -INFINITY;
+        gx[r] = apply_penalty(v, gm[r], rp);
+      }
+    }
+  };
+  auto collect_rest = [&](float tf, uint32_t cnt, uint32_t counter) __attribute__((always_inline)) {
+    uint32_t* rk = s_wkey + wave * kWaveCand;
+    uint32_t* ri = s_wid + wave * kWaveCand;
+#pragma unroll
+    for (uint32_t r = 0; r < kPenPerThread; ++r) {
+      const bool hit = gx[r] >= tf;
+      const uint64_t m = __ballot(hit);
+      if (m) {
+        const uint32_t o = cnt + lanes_below(m);
+        if (hit && o < kWaveCand) {
+          rk[o] = __float_as_uint(gx[r]);
+          ri[o] = gp[r] | 0xff000000u;  // processor value: always valid
+        }
+        cnt += (uint32_t)__popcll((unsigned long long)m);
+      }
+    }
+    if (cnt > kWaveCand) {
+      if (lane == 0) atomicOr(&s_misc[7], 1u);  // region overflow
+      return;
+    }
+    // Settle each hit: owner slots that are penalized (their processor
+    // lane stands in), padding or masked are dropped; the rest get their
+    // post-temperature order key (one division per hit, generate.rs:357-359).
+    for (uint32_t k = lane; k < cnt; k += 64) {
+      const float v = __uint_as_float(rk[k]);
+      const uint32_t w = ri[k];
+      const uint32_t pos = w & 0x00ffffffu, e = w >> 24;
+      bool ok = true;
+      if (e != 0xffu) {
+        // owner slot: the owner's penalized mask lives in LDS
+        ok = pos < V && !((s_pm[pos_owner(pos)] >> e) & 1u) && !(a.allowed && masked_out(a, pos));
+      }
+      const uint64_t mk = __ballot(ok);
+      uint32_t base = 0u;
+      if (lane == 0 && mk) base = atomicAdd(&s_misc[counter], (uint32_t)__popcll((unsigned long long)mk));
+      base = readlane_u32(base, 0);
+      const uint32_t o = base + lanes_below(mk);
+      if (ok && o < kFastCand) s_ord[o] = cand_order(f2key(v / T), pos);
+    }
+  };
+  auto collect = [&](uint32_t th, uint32_t counter) __attribute__((always_inline)) {
+    const float tf = key2f(th);
+    uint32_t cnt = 0u;
+    scan_own(tf, cnt);
+    finish_processors();
+    collect_rest(tf, cnt, counter);
+  };
+  collect(thr, 2);
   lds_barrier();
   uint32_t n = s_misc[2];
-  if (n < K || n > kFastCand) {
-    // The count table is dead by now: it holds the exact histogram.
+  if (n < K || n > kFastCand || s_misc[7]) {
+    // The speculative threshold failed: use the exact one, the lower edge of
+    // the bin holding the K-th largest of the 1024 per-thread maxima (at
+    // least K logits lie at or above it, in the threads whose maximum
+    // does). The count table is dead by now: it holds the histogram.
     uint32_t* bins2 = s_cnt;
     reinterpret_cast<uint4*>(bins2)[tid] = make_uint4(0u, 0u, 0u, 0u);
     float tm = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < NCH * 4; ++e) tm = fmaxf(tm, x[e]);
+    for (int e = 0; e < NCH * 4; ++e) tm = slot_ok(e) ? fmaxf(tm, x[e]) : tm;
 #pragma unroll
     for (uint32_t r = 0; r < kPenPerThread; ++r) tm = fmaxf(tm, gx[r]);
+    if (tid == 0) s_misc[7] = 0u;
     lds_barrier();
     atomicAdd(&bins2[(tm == tm ? f2key(tm) : kKeyNone) >> (32 - kSelBits)], 1u);
     lds_barrier();
     thr = hist_threshold(bins2, s_seg, K, T, wave, lane);
     if (thr <= 0x007fffffu) return false;
-    append(thr, 6);
+    collect(thr, 6);
     lds_barrier();
     n = s_misc[6];
     // Heavy ties or an unusually flat top: not bounded by the register
     // path.
-    if (n > kFastCand) return false;
+    if (n > kFastCand || s_misc[7]) return false;
   }
 
-  // 7. Post-temperature order keys, one division per candidate
-  //    (generate.rs:357-359), then ranks rank(i) = #{j : ord_j > ord_i},
-  //    the j range split over all waves.
-  for (uint32_t i = tid; i < n; i += kBlock) s_ord[i] = cand_order(f2key(key2f(s_ckey[i]) / T), s_cid[i]);
-  lds_barrier();
-  if (n <= kBlock) {
-    const uint32_t n64 = (n + 63u) & ~63u;
-    const uint32_t groups = kBlock / n64;
-    const uint32_t i = tid % n64, g = tid / n64;
-    if (g < groups && i < n) {
-      const uint64_t oi = s_ord[i];
-      const uint32_t j0 = (n * g / groups) & ~1u;
-      const uint32_t j1 = g + 1 == groups ? n : ((n * (g + 1) / groups) & ~1u);
-      uint32_t r = 0u, j = j0;
-      for (; j + 8 <= j1; j += 8) {
-        const ulonglong2 p0 = *reinterpret_cast<const ulonglong2*>(&s_ord[j]);
-        const ulonglong2 p1 = *reinterpret_cast<const ulonglong2*>(&s_ord[j + 2]);
-        const ulonglong2 p2 = *reinterpret_cast<const ulonglong2*>(&s_ord[j + 4]);
-        const ulonglong2 p3 = *reinterpret_cast<const ulonglong2*>(&s_ord[j + 6]);
-        r += (p0.x > oi) + (p0.y > oi) + (p1.x > oi) + (p1.y > oi) + (p2.x > oi) + (p2.y > oi) +
-             (p3.x > oi) + (p3.y > oi);
+  // 7. Ranks by (w key desc, id asc): rank(i) = #{j : ord_j > ord_i}. Each
+  //    wave takes an even slice of the list; lanes hold the whole list (up
+  //    to 4 keys each) and one ballot per lane-slot counts the keys that
+  //    come first.
+  {
+    const uint32_t per = (n + kWaves - 1) / kWaves;
+    const uint32_t i0 = min(n, wave * per), i1 = min(n, i0 + per);
+    if (n <= 256) {
+      uint64_t oj[4];
+#pragma unroll
+      for (uint32_t t = 0; t < 4; ++t) {
+        const uint32_t j = lane + 64u * t;
+        oj[t] = j < n ? s_ord[j] : 0ull;
       }
-      for (; j < j1; ++j) r += s_ord[j] > oi ? 1u : 0u;
-      atomicAdd(&s_rank[i], r);
-    }
-  } else {
-    for (uint32_t i = tid; i < n; i += kBlock) {
-      const uint64_t oi = s_ord[i];
-      uint32_t r = 0u;
-      for (uint32_t j = 0; j < n; ++j) r += s_ord[j] > oi ? 1u : 0u;
-      s_rank[i] = r;
-    }
-  }
-  lds_barrier();
-  for (uint32_t i = tid; i < n; i += kBlock) {
-    const uint32_t r = s_rank[i];
-    if (r < K) {
-      const uint64_t o = s_ord[i];
-      s_skey[r] = (uint32_t)(o >> 32);
-      s_sid[r] = 0xffffffffu - (uint32_t)o;
+      const uint64_t mi = i0 + lane < i1 ? s_ord[i0 + lane] : 0ull;
+      for (uint32_t i = 0; i < i1 - i0; ++i) {
+        const uint64_t oi = readlane_u64(mi, i);
+        uint32_t r = 0u;
+#pragma unroll
+        for (uint32_t t = 0; t < 4; ++t) r += (uint32_t)__popcll((unsigned long long)__ballot(oj[t] > oi));
+        if (r < K && lane == 0) {
+          s_skey[r] = (uint32_t)(oi >> 32);
+          s_sid[r] = 0xffffffffu - (uint32_t)oi;
+        }
+      }
+    } else {
+      for (uint32_t i = i0; i < i1; ++i) {
+        const uint64_t oi = s_ord[i];
+        uint32_t r = 0u;
+        for (uint32_t j0 = 0; j0 < n; j0 += 64) {
+          const uint32_t j = j0 + lane;
+          r += (uint32_t)__popcll((unsigned long long)__ballot(j < n && s_ord[j] > oi));
+        }
+        if (r < K && lane == 0) {
+          s_skey[r] = (uint32_t)(oi >> 32);
+          s_sid[r] = 0xffffffffu - (uint32_t)oi;
+        }
+      }
     }
   }
   lds_barrier();

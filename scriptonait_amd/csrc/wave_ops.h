@@ -49,6 +49,16 @@ __device__ __forceinline__ uint32_t readlane_u32(uint32_t x, uint32_t l) {
   return (uint32_t)__builtin_amdgcn_readlane((int)x, (int)l);
 }
 
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t x, uint32_t l) {
+  const uint32_t lo = readlane_u32((uint32_t)x, l), hi = readlane_u32((uint32_t)(x >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Number of set bits of the wave mask m in lanes below this one.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return (uint32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 // Bit mask of the lanes below this one.
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const uint32_t lane = lane_id();
