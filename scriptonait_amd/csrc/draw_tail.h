@@ -13,18 +13,19 @@
 
 namespace llmhip {
 
-// key_at(i) / id_at(i): i-th candidate (i < n) in sorted order.
+// key_at(i) / id_at(i): i-th candidate (i < n) in sorted order; st is row
+// b's RNG state and tab the exp table (kExp2fTab or an LDS copy of it).
 // Must be called by all 64 lanes of exactly one wave. Writes out_ids,
 // rng_state, out_kept and (if requested) out_probs for row b.
 template <class KeyAt, class IdAt>
 __device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const llmhip_params& P, uint32_t n,
-                          KeyAt key_at, IdAt id_at) {
+                          KeyAt key_at, IdAt id_at, uint64_t st, const uint64_t* tab) {
   const uint32_t lane = lane_id();
   const uint32_t k0 = key_at(0);
   // fold(NEG_INFINITY, f32::max) over sorted candidates: the first one
   // unless it is NaN (NaN keys sort last, so then all are NaN).
   const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
-  auto e_at = [&](uint32_t i) { return glibc_expf(key2f(key_at(i)) - mx); };
+  auto e_at = [&](uint32_t i) { return glibc_expf_tab(key2f(key_at(i)) - mx, tab); };
 
   // generate.rs:374: sum as a left fold in sorted order.
   float sum = 0.0f;
@@ -90,7 +91,6 @@ __device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const
   }
 
   // generate.rs:412-419: r = u * total, walk with r -= p.
-  uint64_t st = a.rng_state[b];
   const float u = next_f32(st);
   float r = u * total;
   uint32_t pick = keep - 1u;
@@ -130,12 +130,12 @@ __device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const
 // decides (the reference's early `break`).
 __device__ __forceinline__ void draw_tail_small(const SampleArgs& a, uint32_t b, const llmhip_params& P,
                                                 uint32_t n, uint32_t my_key, uint32_t my_id,
-                                                uint64_t st, float* buf) {
+                                                uint64_t st, float* buf, const uint64_t* tab) {
   const uint32_t lane = lane_id();
   const bool act = lane < n;
   const uint32_t k0 = readlane_u32(my_key, 0);
   const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
-  const float e = act ? glibc_expf(key2f(my_key) - mx) : 0.0f;
+  const float e = act ? glibc_expf_tab(key2f(my_key) - mx, tab) : 0.0f;
   float* cbuf = buf + 64;
   const float4* b4 = reinterpret_cast<const float4*>(buf);
 

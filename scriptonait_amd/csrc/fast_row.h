@@ -1,0 +1,727 @@
+// Register path of the gfx950 sampler: one row per 1024-thread workgroup,
+// V <= 32768, 0 < top_k <= 1024 (and greedy rows).
+//
+// Row semantics: crates/llm-core/src/generate.rs:325-420. The row is read
+// once from HBM into registers; the work that decides the sample runs while
+// the row streams in, and only a compare, one settle pass, two workgroup
+// barriers, a rank over ~2K candidates and the sequential tail remain after
+// the last byte lands.
+//
+// Layout. Wave w owns the contiguous 1 KiB blocks w*NCH .. w*NCH+NCH-1 of
+// the row (256 floats each); lane l of wave w holds block (w*NCH + c)'s
+// floats 4l..4l+3 as its chunk c, loaded with one nontemporal dwordx4. Every
+// load is 1 KiB contiguous per wave, and the first S chunks of all waves
+// form a sample spread evenly over the whole row.
+//
+// Streaming. A wave keeps D chunks in flight: chunk c+D is issued when chunk
+// c has landed. That keeps the HBM queues as full as issuing everything at
+// once would, but the chunks land in order, so the sample is complete early
+// and the scan keeps pace with the data.
+//
+// Throughput. The 16 waves of a workgroup share one CU: one scalar unit and
+// four SIMDs. Work that every wave would repeat (the threshold) is done by
+// one wave, and per-chunk work is a compare and a rare append.
+//
+// Per wave:
+//  1. chunks 0..S-1 land: per-thread maximum of the sample.
+//  2. LDS barrier (tables zeroed); the maxima go into a two-level key
+//     histogram; the wave signals. The wave that signals last selects the
+//     speculative threshold (about 2K of the row's values expected at or
+//     above it) and publishes it in LDS.
+//  3. history ids are counted: u16 multiplicities and per-owner masks of
+//     penalized slots, integer LDS atomics whose result does not depend on
+//     order.
+//  4. each landed chunk is compared with the threshold once it is published
+//     (chunks that landed before are caught up); hits go to the wave's LDS
+//     region.
+//  5. after the last chunk, the wave settles its hits (mask, penalty m times
+//     in sequence, recheck, one division by T) into the candidate list.
+//  6. barrier; the count check (>= K proves the threshold); rank; barrier.
+//  7. one wave replays the reference's folds and draws.
+//
+// Selecting on raw values is exact: the mask sets -inf and a penalty
+// p >= 1 never raises a value (l/p <= l for l > 0, l*p <= l for l <= 0,
+// each correctly rounded), so every value at or above the threshold after
+// mask and penalty was at or above it before. For p < 1 (or NaN) the values
+// are fixed up before the compare instead.
+#pragma once
+#include <type_traits>
+
+#include "draw_tail.h"
+#include "sampler_common.h"
+#include "wave_ops.h"
+
+// Profiling hooks: a profiling build defines LLMHIP_MARK(i) (a timestamp
+// per wave at phase i) and LLMHIP_NOTE(i, v) (a recorded value); both are
+// empty otherwise.
+#ifndef LLMHIP_MARK
+#define LLMHIP_MARK(i)
+#endif
+#ifndef LLMHIP_NOTE
+#define LLMHIP_NOTE(i, v)
+#endif
+
+namespace llmhip {
+
+// LDS needed by the general path (about 20 KB).
+struct GenLds {
+  uint32_t bins[256];
+  uint32_t off[256];
+  uint32_t wc[kWaves * 256];
+  float redv[kWaves];
+  uint32_t redi[kWaves];
+  uint64_t exptab[32];
+};
+
+constexpr uint32_t kFastCand = 2048;              // candidates per row
+constexpr uint32_t kRegion = kFastCand / kWaves;  // raw hits per wave
+constexpr uint32_t kHistPerThread = 2;            // history ids fetched per thread up front
+constexpr uint32_t kCoarseBins = 256;             // key bits 31..24
+constexpr uint32_t kFineBins = 4096;              // key bits 31..20
+constexpr uint32_t kSpecScale = 2;                // speculative threshold aims at ~kSpecScale*K values
+
+// misc[] slots
+constexpr int kSyncSample = 0;  // waves whose sample is in the histogram
+constexpr int kSyncHist = 1;    // waves whose history ids are counted
+constexpr int kCandN = 2;       // candidates in ord[]
+constexpr int kOverflow = 3;    // some wave's region overflowed
+constexpr int kTauState = 4;    // 0: not yet, 1: published in kTauKey, 2: row not bounded here
+constexpr int kTauKey = 5;
+
+template <int NCH>
+struct FastLds {
+  union {
+    uint32_t cnt[NCH * 2048];  // u16 history multiplicities, two per word (V <= NCH*4096)
+    GenLds gen;                // the general path's LDS when a row falls back
+  };
+  uint32_t pm[kBlock];  // per-thread mask: slot is penalized
+  __attribute__((aligned(16))) uint32_t coarse[kCoarseBins];
+  __attribute__((aligned(16))) uint32_t fine[kFineBins];
+  uint32_t rv[kFastCand];    // raw hit value bits, per-wave regions
+  uint32_t rpos[kFastCand];  // raw hit position | slot << 24
+  uint64_t ord[kFastCand];   // settled order keys
+  uint32_t skey[kMaxFastK];  // sorted top-K: post-temperature key
+  uint32_t sid[kMaxFastK];   //               id
+  uint64_t exptab[32];
+  __attribute__((aligned(16))) float tail[128];
+  float redv[kWaves];
+  uint32_t redi[kWaves];
+  uint32_t misc[16];
+};
+
+// Read-only inputs that every lane of a wave reads at the same address go
+// through the constant address space, so they become scalar (SMEM) loads:
+// those count on lgkmcnt and never queue behind the row's vector loads.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* as_const(const T* p) {
+  return (const __attribute__((address_space(4))) T*)p;
+}
+
+__device__ __forceinline__ llmhip_params load_params(const SampleArgs& a, uint32_t b) {
+  llmhip_params P = a.shared;
+  if (a.params) {
+    const auto* q = as_const(a.params) + (size_t)b * a.params_stride;
+    P.temperature = q->temperature;
+    P.top_k = q->top_k;
+    P.top_p = q->top_p;
+    P.min_p = q->min_p;
+    P.repetition_penalty = q->repetition_penalty;
+  }
+  return P;
+}
+
+__device__ __forceinline__ float apply_penalty(float v, uint32_t m, float rp) {
+  // generate.rs:343-352, once per occurrence, in sequence.
+  for (; m; --m) v = v > 0.0f ? v / rp : v * rp;
+  return v;
+}
+
+__device__ __forceinline__ bool masked_out(const SampleArgs& a, uint32_t id) {
+  // generate.rs:333-341
+  return a.allowed && id < a.allowed_len && id != a.eos_id && a.allowed[id] == 0;
+}
+
+// Block-wide argmax of (bv, bi) pairs; every thread must call. Returns the
+// winner in all threads of wave 0 (UINT32_MAX when no thread had a value).
+__device__ __forceinline__ uint32_t block_argmax(float bv, uint32_t bi, float* redv,
+                                                 uint32_t* redi) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  wave_argmax(bv, bi);
+  if (lane == 0) {
+    redv[wave] = bv;
+    redi[wave] = bi;
+  }
+  __syncthreads();
+  float v = lane < kWaves ? redv[lane] : -INFINITY;
+  uint32_t i = lane < kWaves ? redi[lane] : 0xffffffffu;
+  wave_argmax(v, i);
+  return i;
+}
+
+// Workgroup barrier that orders LDS only: outstanding global loads stay in
+// flight across it (a full __syncthreads would wait for every row load).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One wave announces that its LDS writes so far are complete (LDS-only
+// release: no wait on the wave's outstanding global loads). Returns the
+// number of waves that had signalled before, in every lane.
+__device__ __forceinline__ uint32_t lds_signal(uint32_t* ctr) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  uint32_t before = 0u;
+  if ((threadIdx.x & 63u) == 0u) before = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  return readlane_u32(before, 0);
+}
+
+__device__ __forceinline__ uint32_t lds_peek(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Wait until *ctr >= target. Every wave that counts toward a target signals
+// it unconditionally before it waits on anything, so the wait ends. The
+// spin is bounded all the same (about 0.1 s): should that ever run out (a
+// bug, not an input condition), the wave records it in the call's status
+// word and carries on, so the kernel still finishes and the host entry
+// reports the failure instead of the GPU hanging.
+constexpr uint32_t kSpinLimit = 1u << 20;
+__device__ __forceinline__ void lds_wait(const uint32_t* ctr, uint32_t target, uint32_t* status) {
+  uint32_t spins = 0;
+  while (lds_peek(ctr) < target) {
+    if (++spins > kSpinLimit) {
+      if ((threadIdx.x & 63u) == 0u) atomicOr(status, kStatusSyncTimeout);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Row position of chunk c's first float in lane `lane` of wave `wave`.
+template <int NCH>
+__device__ __forceinline__ uint32_t chunk_pos(uint32_t c, uint32_t wave, uint32_t lane) {
+  return ((wave * NCH + c) * 64u + lane) * 4u;
+}
+template <int NCH>
+__device__ __forceinline__ uint32_t pos_owner(uint32_t p) {
+  return ((p >> 8) / NCH) * 64u + ((p >> 2) & 63u);
+}
+template <int NCH>
+__device__ __forceinline__ uint32_t pos_slot(uint32_t p) {
+  return ((p >> 8) % NCH) * 4u + (p & 3u);
+}
+
+// Candidate order key: larger = earlier in the reference's sort (value
+// desc, then id asc, generate.rs:364-367).
+__device__ __forceinline__ uint64_t cand_order(uint32_t wkey, uint32_t id) {
+  return ((uint64_t)wkey << 32) | (uint64_t)(0xffffffffu - id);
+}
+
+// f(integral_constant<int, I>) for I = I0 .. N-1, expanded at compile time
+// (chunk indices must be constants: the row lives in registers).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Lane i < 32 gets kExp2fTab[i] from instruction immediates: no memory
+// access, so the table never waits behind the row's loads.
+__device__ __forceinline__ uint64_t exp2f_tab_lane(uint32_t lane) {
+  uint64_t v = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v = lane == (uint32_t)i ? kExp2fTab[i] : v;
+  return v;
+}
+
+// The Q-th largest key counted in the two-level histogram (coarse: key bits
+// 31..24, fine: bits 31..20), as a key threshold. exact: the lower edge of
+// the fine bin holding it, so at least Q counted keys lie at or above the
+// result. Otherwise an estimate inside that bin, taking its keys as evenly
+// spread. Returns 0 when fewer than Q keys were counted. Wave-local.
+__device__ __forceinline__ uint32_t hist_select(const uint32_t* coarse, const uint32_t* fine, uint32_t Q,
+                                                bool exact, uint32_t lane) {
+  // Lane l holds coarse bins 255-4l .. 252-4l (w, z, y, x: descending).
+  const uint4 q = reinterpret_cast<const uint4*>(coarse)[63u - lane];
+  const uint32_t lt = q.x + q.y + q.z + q.w;
+  const uint32_t ci = wave_incl_scan(lt);
+  const uint64_t lm = __ballot(Q <= ci);
+  if (!lm) return 0u;
+  const uint32_t l = (uint32_t)__ffsll((unsigned long long)lm) - 1u;
+  uint32_t need = Q - (readlane_u32(ci, l) - readlane_u32(lt, l));
+  const uint32_t cw = readlane_u32(q.w, l), cz = readlane_u32(q.z, l), cy = readlane_u32(q.y, l);
+  uint32_t cb = 255u - 4u * l;
+  if (need > cw) {
+    need -= cw;
+    --cb;
+    if (need > cz) {
+      need -= cz;
+      --cb;
+      if (need > cy) {
+        need -= cy;
+        --cb;
+      }
+    }
+  }
+  // Lanes 0..15 hold the 16 fine bins of coarse bin cb, descending.
+  const uint32_t fc = lane < 16u ? fine[cb * 16u + 15u - lane] : 0u;
+  const uint32_t fi = wave_incl_scan(fc);
+  const uint64_t fm = __ballot(lane < 16u && need <= fi);
+  const uint32_t fl = (uint32_t)__ffsll((unsigned long long)fm) - 1u;
+  const uint32_t lo = (cb * 16u + 15u - fl) << 20;
+  if (exact) return lo;
+  const uint32_t cnt = readlane_u32(fc, fl);
+  const uint32_t need2 = need - (readlane_u32(fi, fl) - cnt);  // 1..cnt
+  // need2 <= cnt <= 1024, so need2 << 20 fits in 32 bits.
+  return lo + (1u << 20) - (need2 << 20) / (cnt + 1u);
+}
+
+// Lower a raw-value key threshold past every key whose value divided by T
+// ties with it (division can merge distinct values, and the reference then
+// orders the merged ones by id). Lane l tests the key l+1 below; runs of
+// ties are at most ceil(2T)+1 keys long, so 64 covers T < 31. Returns 0
+// when the row is not bounded this way (threshold at or below -inf, or a
+// longer run).
+__device__ __forceinline__ uint32_t lower_past_ties(uint32_t tau, float T, uint32_t lane) {
+  if (tau <= 0x007fffffu + 64u) return 0u;
+  const uint32_t wt = f2key(key2f(tau) / T);
+  const uint64_t ties = __ballot(f2key(key2f(tau - 1u - lane) / T) == wt);
+  const uint64_t run = ~ties;
+  if (run == 0ull) return 0u;
+  const uint32_t lo = tau - ((uint32_t)__ffsll((unsigned long long)run) - 1u);
+  return lo > 0x007fffffu ? lo : 0u;
+}
+
+// Ranks of the n candidates in ord[] (order keys, all distinct): rank(i) =
+// #{j : ord_j > ord_i}; the K best are written to skey/sid in sorted order.
+// All 16 waves share the candidates; each wave holds the whole list in
+// registers (NR keys per lane) and ranks an even slice of it, one ballot
+// per held key. Lane i collects candidate i's rank, so the loop body
+// touches no LDS and waits on nothing.
+template <int NR>
+__device__ __forceinline__ void rank_in_regs(const uint64_t* ord, uint32_t n, uint32_t K, uint32_t wave,
+                                             uint32_t lane, uint32_t* skey, uint32_t* sid) {
+  uint64_t oj[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+    const uint32_t j = lane + 64u * t;
+    oj[t] = j < n ? ord[j] : 0ull;
+  }
+  const uint32_t per = (n + kWaves - 1) / kWaves;  // <= 4 * NR
+  const uint32_t i0 = min(n, wave * per), cnt = min(n, i0 + per) - i0;
+  const uint64_t mi = lane < cnt ? ord[i0 + lane] : 0ull;
+  uint32_t myr = 0xffffffffu;
+  for (uint32_t i = 0; i < cnt; ++i) {
+    const uint64_t oi = readlane_u64(mi, i);
+    uint32_t r = 0u;
+#pragma unroll
+    for (int t = 0; t < NR; ++t) r += (uint32_t)__popcll((unsigned long long)__ballot(oj[t] > oi));
+    myr = lane == i ? r : myr;
+  }
+  if (lane < cnt && myr < K) {
+    skey[myr] = (uint32_t)(mi >> 32);
+    sid[myr] = 0xffffffffu - (uint32_t)mi;
+  }
+}
+
+__device__ __forceinline__ void rank_in_lds(const uint64_t* ord, uint32_t n, uint32_t K, uint32_t wave,
+                                            uint32_t lane, uint32_t* skey, uint32_t* sid) {
+  const uint32_t per = (n + kWaves - 1) / kWaves;
+  const uint32_t i0 = min(n, wave * per), i1 = min(n, i0 + per);
+  for (uint32_t i = i0; i < i1; ++i) {
+    const uint64_t oi = ord[i];
+    uint32_t r = 0u;
+    for (uint32_t j0 = 0; j0 < n; j0 += 64) {
+      const uint32_t j = j0 + lane;
+      r += (uint32_t)__popcll((unsigned long long)__ballot(j < n && ord[j] > oi));
+    }
+    if (r < K && lane == 0) {
+      skey[r] = (uint32_t)(oi >> 32);
+      sid[r] = 0xffffffffu - (uint32_t)oi;
+    }
+  }
+}
+
+// One row on the register path. Returns false (uniformly across the
+// workgroup, before writing any output) when the row needs the general
+// path.
+template <int NCH, bool VEC>
+__device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
+  static_assert(NCH * 4 <= 32, "slot masks are 32 bits");
+  constexpr int S = NCH >= 4 ? NCH / 4 : 1;  // sample chunks per wave
+  constexpr int D = NCH >= 2 ? 2 : 1;        // chunks in flight per wave
+  typedef float f4v __attribute__((ext_vector_type(4)));
+
+  // The grid is exactly B workgroups.
+  const uint32_t b = blockIdx.x;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  const uint32_t V = a.V;
+  LLMHIP_MARK(0);
+
+  // Every global load below is issued unconditionally (positions past V and
+  // absent inputs read a valid dummy address), so each wait in the compiled
+  // code names exactly the loads it needs.
+  const float* row = a.logits + (size_t)b * a.ld;
+  float x[NCH * 4];
+  auto load_chunk = [&](int c) __attribute__((always_inline)) {
+    const uint32_t base = chunk_pos<NCH>((uint32_t)c, wave, lane);
+    if (VEC) {
+      const f4v q = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(row + (base < V ? base : 0u)));
+      x[4 * c + 0] = q.x;
+      x[4 * c + 1] = q.y;
+      x[4 * c + 2] = q.z;
+      x[4 * c + 3] = q.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * c + j] = __builtin_nontemporal_load(row + (base + j < V ? base + j : 0u));
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < D; ++c) load_chunk(c);
+  const uint32_t mkbits = a.slotmask[tid];  // masked-out slots (allowed mask), or 0
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t h0 = 0, h1 = 0;
+  if (a.hist_offsets && a.hist) {
+    h0 = as_const(a.hist_offsets)[b];
+    h1 = as_const(a.hist_offsets)[b + 1];
+  }
+  const llmhip_params P = load_params(a, b);
+  const uint64_t rng0 = as_const(a.rng_state)[b];
+
+  // LDS set-up (the count table only when a history may be used).
+  if (wave == 0 && lane < 32) L.exptab[lane] = exp2f_tab_lane(lane);
+  if (a.hist) {
+    uint4* c4 = reinterpret_cast<uint4*>(L.cnt);
+    for (uint32_t i = tid; i < (V + 7u) / 8u; i += kBlock) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);  // kFineBins / 4 == kBlock
+  if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
+  L.pm[tid] = 0u;
+  if (tid < 16) L.misc[tid] = 0u;
+
+  auto chunk_full = [&](int c) __attribute__((always_inline)) {
+    return (wave * NCH + (uint32_t)c + 1u) * 256u <= V;
+  };
+  auto slot_valid = [&](int e) __attribute__((always_inline)) {
+    return chunk_full(e >> 2) || chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3) < V;
+  };
+
+  // 1. Sample: chunks 0..S-1 as they land; chunk c+D goes out as chunk c
+  //    arrives.
+  float sm = -INFINITY;
+  static_for<0, S>([&](auto cc) __attribute__((always_inline)) {
+    constexpr int c = decltype(cc)::value;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sm = slot_valid(4 * c + j) ? fmaxf(sm, x[4 * c + j]) : sm;
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (c + D < NCH) load_chunk(c + D);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  lds_barrier();  // LDS tables are zeroed
+  LLMHIP_MARK(1);
+
+  const uint32_t cls = row_class(P, V);
+  if (!(cls & a.row_class_mask)) return true;
+  const float T = P.temperature, rp = P.repetition_penalty;
+  const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
+  if (H >= 65536u) return false;  // a u16 multiplicity could overflow
+  const bool use_pen = H > 0;
+  const bool greedy = cls == kClassGreedy;
+  const uint32_t K = P.top_k;  // 0 < K < V, K <= kMaxFastK unless greedy (row class)
+
+  // Every wave fetches a slice of the history ids (counted a little later,
+  // when they have landed).
+  uint32_t hid[kHistPerThread];
+  {
+    const uint32_t* hsrc = use_pen ? a.hist + h0 : a.slotmask;
+    const uint32_t hmax = use_pen ? H - 1u : 0u;
+#pragma unroll
+    for (uint32_t u = 0; u < kHistPerThread; ++u) {
+      const uint32_t j = tid + u * kBlock;
+      hid[u] = hsrc[j < hmax ? j : hmax];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. Sample maxima into the histogram; the last wave to arrive selects the
+  //    speculative threshold. Q scales the target kSpecScale*K to the sample.
+  if (!greedy && sm > -INFINITY) {  // NaN and -inf maxima are not counted
+    const uint32_t k = f2key(sm);
+    atomicAdd(&L.coarse[k >> 24], 1u);
+    atomicAdd(&L.fine[k >> 20], 1u);
+  }
+  if (lds_signal(&L.misc[kSyncSample]) == kWaves - 1u && !greedy) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    LLMHIP_MARK(3);
+    const bool whole = S == NCH;
+    const uint32_t Q =
+        whole ? K : (uint32_t)(((uint64_t)kSpecScale * K * a.spec_sampled + V - 1u) / V) + 2u;
+    const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, Q, whole, lane), T, lane);
+    if (lane == 0) {
+      L.misc[kTauKey] = tkey;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      __hip_atomic_store(&L.misc[kTauState], tkey ? 1u : 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  LLMHIP_MARK(2);
+
+  auto count_of = [&](uint32_t p) __attribute__((always_inline)) {
+    return (L.cnt[p >> 1] >> ((p & 1u) << 4)) & 0xffffu;
+  };
+  auto add_hist = [&](uint32_t id) __attribute__((always_inline)) {
+    if (id < V) {
+      const uint32_t sh = (id & 1u) << 4;
+      const uint32_t old = atomicAdd(&L.cnt[id >> 1], 1u << sh);
+      if (((old >> sh) & 0xffffu) == 0u) atomicOr(&L.pm[pos_owner<NCH>(id)], 1u << pos_slot<NCH>(id));
+    }
+  };
+  // Mask and penalty of this thread's slot e, in the reference's order.
+  auto fix_value = [&](float v, int e, uint32_t pmv) __attribute__((always_inline)) {
+    if ((mkbits >> e) & 1u) v = -INFINITY;
+    if ((pmv >> e) & 1u) v = apply_penalty(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3)), rp);
+    return v;
+  };
+  auto fix_chunk = [&](int c, uint32_t pmv) __attribute__((always_inline)) {
+    if ((((pmv | mkbits) >> (4 * c)) & 0xfu) != 0u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * c + j] = fix_value(x[4 * c + j], 4 * c + j, pmv);
+    }
+  };
+
+  // Modes of a scan: kRaw compares raw values (hits are settled with mask
+  // and penalty afterwards); kFixFirst fixes every slot before its compare
+  // (a penalty p < 1 can raise a value); kFinal compares final values.
+  enum { kRaw = 0, kFixFirst = 1, kFinal = 2 };
+  const int mode0 = (use_pen && !(rp >= 1.0f)) ? kFixFirst : kRaw;
+  uint32_t pmv = 0u;
+  float tf = 0.0f;
+  uint32_t hits = 0u;  // this wave's raw hits so far
+  // Hits of chunk c: one compare per logit; for the rare chunks where some
+  // lane hits, a ballot offset and two LDS writes into the wave's region.
+  auto scan_chunk = [&](int c, int mode) __attribute__((always_inline)) {
+    if (mode == kFixFirst) fix_chunk(c, pmv);
+    const uint32_t base = chunk_pos<NCH>((uint32_t)c, wave, lane);
+    bool hit[4];
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hit[j] = x[4 * c + j] >= tf;
+      if (!chunk_full(c)) hit[j] = hit[j] && base + j < V;
+      any = any || hit[j];
+    }
+    if (__ballot(any)) {
+      uint32_t* rvw = L.rv + wave * kRegion;
+      uint32_t* rpw = L.rpos + wave * kRegion;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint64_t m = __ballot(hit[j]);
+        const uint32_t o = hits + lanes_below(m);
+        if (hit[j] && o < kRegion) {
+          rvw[o] = __float_as_uint(x[4 * c + j]);
+          rpw[o] = (base + j) | ((uint32_t)(4 * c + j) << 24);
+        }
+        hits += (uint32_t)__popcll((unsigned long long)m);
+      }
+    }
+  };
+  // Settle this wave's hits: mask, penalty (kRaw only), recheck, and the
+  // post-temperature order key (one division, generate.rs:357-359), appended
+  // to ord[] with one LDS atomic per 64 hits.
+  auto settle = [&](int mode) __attribute__((always_inline)) {
+    if (hits > kRegion) {
+      if (lane == 0) atomicOr(&L.misc[kOverflow], 1u);
+      return;
+    }
+    const uint32_t* rvw = L.rv + wave * kRegion;
+    const uint32_t* rpw = L.rpos + wave * kRegion;
+    for (uint32_t k0 = 0; k0 < hits; k0 += 64u) {
+      const uint32_t k = k0 + lane;
+      bool ok = k < hits;
+      const uint32_t tag = ok ? rpw[k] : 0u;
+      float v = ok ? __uint_as_float(rvw[k]) : 0.0f;
+      const uint32_t pos = tag & 0x00ffffffu;
+      if (mode == kRaw) {
+        // The hit's owner is a lane of this wave: fetch its mask word.
+        const uint32_t e = tag >> 24;
+        const uint32_t owner = pos_owner<NCH>(pos);
+        const uint32_t mkown = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((owner & 63u) << 2), (int)mkbits);
+        if (ok) {
+          if ((mkown >> e) & 1u) v = -INFINITY;
+          if (use_pen && ((L.pm[owner] >> e) & 1u)) v = apply_penalty(v, count_of(pos), rp);
+          ok = v >= tf;
+        }
+      }
+      const uint64_t mk = __ballot(ok);
+      if (mk) {
+        uint32_t o = 0u;
+        if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
+        o = readlane_u32(o, 0) + lanes_below(mk);
+        if (ok && o < kFastCand) L.ord[o] = cand_order(f2key(v / T), pos);
+      }
+    }
+  };
+
+  // 3-4. History counts, then the scan of every chunk as soon as both it
+  //    and the threshold are there. Step c runs when chunk c has landed
+  //    (the compiler waits for it at its first use); step NCH closes.
+  constexpr int CH = S + 1 < NCH ? S + 1 : NCH;  // step that counts the history
+  uint32_t scanned = 0u;  // chunks scanned so far
+  uint32_t tau = 0u;      // 0: not yet, 1: threshold in tf, 2: not bounded
+  static_for<S, NCH + 1>([&](auto cc) __attribute__((always_inline)) {
+    constexpr int c = decltype(cc)::value;
+    if constexpr (c < NCH) {
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (c + D < NCH) load_chunk(c + D);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (c == CH) {
+      // History multiplicities (the ids have landed by now). The first
+      // occurrence of an id marks its slot in the owner thread's mask.
+      if (use_pen) {
+#pragma unroll
+        for (uint32_t u = 0; u < kHistPerThread; ++u)
+          if (tid + u * kBlock < H) add_hist(hid[u]);
+        for (uint32_t j = tid + kHistPerThread * kBlock; j < H; j += kBlock) add_hist(a.hist[h0 + j]);
+      }
+      lds_signal(&L.misc[kSyncHist]);
+    }
+    if (greedy || tau == 2u) return;
+    if (tau == 0u) {
+      // kFixFirst waits below for every wave's history counts, so it may
+      // start only once this wave has counted its own (step CH).
+      if (mode0 == kFixFirst && c < CH) return;
+      if constexpr (c == NCH) lds_wait(&L.misc[kTauState], 1u, a.status);
+      tau = lds_peek(&L.misc[kTauState]);
+      if (tau != 1u) return;  // not published yet (scan later), or not bounded
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+      tf = key2f(L.misc[kTauKey]);
+      if (mode0 == kFixFirst) {
+        lds_wait(&L.misc[kSyncHist], kWaves, a.status);
+        pmv = L.pm[tid];
+      }
+      LLMHIP_MARK(4);
+    }
+    // Chunks scanned..min(c, NCH-1) have landed: scan them.
+    static_for<0, (c < NCH ? c + 1 : NCH)>([&](auto qq) __attribute__((always_inline)) {
+      constexpr int q = decltype(qq)::value;
+      if (scanned <= (uint32_t)q) scan_chunk(q, mode0);
+    });
+    scanned = c < NCH ? c + 1 : NCH;
+  });
+  LLMHIP_MARK(5);
+
+  if (greedy) {
+    // ops/loss.rs:6-16 over the masked, penalized row (before temperature).
+    if (use_pen) {
+      lds_wait(&L.misc[kSyncHist], kWaves, a.status);
+      pmv = L.pm[tid];
+    }
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      fix_chunk(c, pmv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * c + j;
+        if (x[e] > bv && slot_valid(e)) {
+          bv = x[e];
+          bi = chunk_pos<NCH>((uint32_t)c, wave, lane) + j;
+        }
+      }
+    }
+    const uint32_t w = block_argmax(bv, bi, L.redv, L.redi);
+    if (tid == 0) {
+      a.out_ids[b] = w == 0xffffffffu ? 0u : w;
+      if (a.out_kept) a.out_kept[b] = 0u;
+    }
+    return true;
+  }
+  if (tau == 2u) return false;  // every wave read the same state
+
+  if (use_pen && mode0 == kRaw) {
+    lds_wait(&L.misc[kSyncHist], kWaves, a.status);
+    pmv = L.pm[tid];
+  }
+  settle(mode0);
+  lds_barrier();
+  LLMHIP_MARK(6);
+  uint32_t n = L.misc[kCandN];
+  LLMHIP_NOTE(12, n);
+  if (n < K || n > kFastCand || L.misc[kOverflow]) {
+    LLMHIP_NOTE(13, 1);
+    // The speculative threshold failed: use the exact one, the lower edge of
+    // the fine bin holding the K-th largest of the 1024 per-thread maxima of
+    // the masked, penalized row (at least K values lie at or above it, in
+    // the threads whose maximum does). Everyone is past the sample
+    // histogram, so it is reused.
+    float tm = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (mode0 == kRaw) fix_chunk(c, pmv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tm = slot_valid(4 * c + j) ? fmaxf(tm, x[4 * c + j]) : tm;
+    }
+    reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 0) {
+      L.misc[kCandN] = 0u;
+      L.misc[kOverflow] = 0u;
+    }
+    lds_barrier();
+    if (tm > -INFINITY) {
+      const uint32_t k = f2key(tm);
+      atomicAdd(&L.coarse[k >> 24], 1u);
+      atomicAdd(&L.fine[k >> 20], 1u);
+    }
+    lds_barrier();
+    const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, K, true, lane), T, lane);
+    if (tkey == 0u) return false;
+    tf = key2f(tkey);
+    // Values are final now (fixed in place).
+    hits = 0u;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) scan_chunk(c, kFinal);
+    settle(kFinal);
+    lds_barrier();
+    n = L.misc[kCandN];
+    // Heavy ties or an unusually flat top: not bounded by the register path.
+    if (n < K || n > kFastCand || L.misc[kOverflow]) return false;
+  }
+
+  // 6. Ranks by (w key desc, id asc).
+  LLMHIP_MARK(9);
+  if (n <= 128) {
+    rank_in_regs<2>(L.ord, n, K, wave, lane, L.skey, L.sid);
+  } else if (n <= 256) {
+    rank_in_regs<4>(L.ord, n, K, wave, lane, L.skey, L.sid);
+  } else if (n <= 512) {
+    rank_in_regs<8>(L.ord, n, K, wave, lane, L.skey, L.sid);
+  } else {
+    rank_in_lds(L.ord, n, K, wave, lane, L.skey, L.sid);
+  }
+  LLMHIP_MARK(10);
+  lds_barrier();
+  LLMHIP_MARK(7);
+
+  // 7. The sequential tail (one wave).
+  if (wave == 0) {
+    if (K <= 64) {
+      draw_tail_small(a, b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u, rng0,
+                      L.tail, L.exptab);
+    } else {
+      draw_tail(a, b, P, K, [&](uint32_t i) { return L.skey[i]; }, [&](uint32_t i) { return L.sid[i]; }, rng0,
+                L.exptab);
+    }
+  }
+  LLMHIP_MARK(8);
+  return true;
+}
+
+}  // namespace llmhip

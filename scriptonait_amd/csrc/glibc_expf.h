@@ -29,10 +29,8 @@
 
 #if defined(__HIPCC__)
 #define LLMHIP_HD __host__ __device__ __forceinline__
-#define LLMHIP_CONST __constant__
 #else
 #define LLMHIP_HD static inline
-#define LLMHIP_CONST static const
 #endif
 
 #ifndef LLMHIP_EXPF_FUSED
@@ -41,7 +39,9 @@
 
 namespace llmhip {
 
-LLMHIP_CONST uint64_t kExp2fTab[32] = {
+// A constexpr table: device code reads it only with compile-time indices
+// (the values become instruction immediates) and copies it to LDS.
+constexpr uint64_t kExp2fTab[32] = {
     0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
     0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
     0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
@@ -73,8 +73,10 @@ LLMHIP_HD uint64_t f64_bits(double x) {
   return u;
 }
 
-// exp of a binary32 value, bit-identical to glibc 2.35's expf (FMA variant).
-LLMHIP_HD float glibc_expf(float x) {
+// exp of a binary32 value, bit-identical to glibc 2.35's expf (FMA variant),
+// with the 2^(i/32) table read from `tab` (kExp2fTab, or a copy of it that a
+// kernel staged in LDS so the lookup never waits behind streaming loads).
+LLMHIP_HD float glibc_expf_tab(float x, const uint64_t* tab) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   const double kShift = 0x1.8p+52;
   const double kC0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
@@ -96,7 +98,7 @@ LLMHIP_HD float glibc_expf(float x) {
   const uint64_t ki = f64_bits(kd);
   kd -= kShift;
   const double r = __builtin_fma(kInvLn2N, xd, -kd);
-  uint64_t t = kExp2fTab[ki % 32];
+  uint64_t t = tab[ki % 32];
   t += ki << 47;
   const double s = f64_from_bits(t);
   const double z = __builtin_fma(kC0, r, kC1);
@@ -111,7 +113,7 @@ LLMHIP_HD float glibc_expf(float x) {
   const uint64_t ki = f64_bits(kd);
   kd -= kShift;
   const double r = z - kd;
-  uint64_t t = kExp2fTab[ki % 32];
+  uint64_t t = tab[ki % 32];
   t += ki << 47;
   const double s = f64_from_bits(t);
   z = kC0 * r + kC1;
@@ -122,5 +124,10 @@ LLMHIP_HD float glibc_expf(float x) {
   return (float)y;
 #endif
 }
+
+#if !defined(__HIPCC__)
+// Host form (the exhaustive comparison with glibc compiles this one).
+static inline float glibc_expf(float x) { return glibc_expf_tab(x, kExp2fTab); }
+#endif
 
 }  // namespace llmhip

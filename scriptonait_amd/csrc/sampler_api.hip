@@ -14,6 +14,7 @@
 namespace llmhip {
 hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s);
 hipError_t launch_general(const SampleArgs& a, hipStream_t s);
+hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 }  // namespace llmhip
 
 using namespace llmhip;
@@ -75,6 +76,9 @@ struct llmhip_ctx {
   hipStream_t stream = nullptr;  // used by the host entry
   DevBuf scratch;                // general-path per-row scratch
   DevBuf params;                 // per-row params copied from the host
+  DevBuf zeros;                  // kBlock zero words: the fast path's "no mask" slot mask
+  DevBuf slotmask;               // kBlock words: the allowed mask in the fast path's layout
+  DevBuf status;                 // one word of kStatus* bits set by the kernels (zero when all is well)
   // staging of the host entry
   DevBuf logits, hist, hoff, allowed, rng, ids, probs, kept;
 };
@@ -157,6 +161,9 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.out_ids = out_ids;
   a.out_probs = out_probs;
   a.out_kept = out_kept;
+  a.slotmask = static_cast<const uint32_t*>(ctx->zeros.ptr);
+  a.spec_sampled = V <= kMaxFastV ? fast_spec_sampled((uint32_t)V) : 0u;
+  a.status = static_cast<uint32_t*>(ctx->status.ptr);
   a.scratch = static_cast<uint32_t*>(ctx->scratch.ptr);
   a.scratch_row_words = row_words;
 
@@ -165,6 +172,11 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   // last float4 must not extend past its V logits).
   const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0) && (V % 4 == 0);
   if (fast_mask) {
+    if (a.allowed) {
+      if ((st = ctx->slotmask.ensure(kBlock * sizeof(uint32_t)))) return st;
+      HIP_TRY(launch_slotmask(a, static_cast<uint32_t*>(ctx->slotmask.ptr), s));
+      a.slotmask = static_cast<const uint32_t*>(ctx->slotmask.ptr);
+    }
     a.row_class_mask = fast_mask;
     HIP_TRY(launch_fast(a, vec, s));
   }
@@ -229,6 +241,20 @@ int llmhip_ctx_create(int device, llmhip_ctx** out_ctx) {
     delete ctx;
     return hip_fail(e, "hipStreamCreateWithFlags");
   }
+  int st = ctx->zeros.ensure(kBlock * sizeof(uint32_t));
+  if (st == LLMHIP_OK) st = ctx->status.ensure(sizeof(uint32_t));
+  if (st == LLMHIP_OK) {
+    e = hipMemset(ctx->zeros.ptr, 0, kBlock * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(ctx->status.ptr, 0, sizeof(uint32_t));
+    if (e != hipSuccess) st = hip_fail(e, "hipMemset");
+  }
+  if (st != LLMHIP_OK) {
+    ctx->zeros.release();
+    ctx->status.release();
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return st;
+  }
   *out_ctx = ctx;
   return LLMHIP_OK;
 }
@@ -238,8 +264,8 @@ int llmhip_ctx_destroy(llmhip_ctx* ctx) {
   Device d(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   (void)hipDeviceSynchronize();
-  for (DevBuf* b : {&ctx->scratch, &ctx->params, &ctx->logits, &ctx->hist, &ctx->hoff,
-                    &ctx->allowed, &ctx->rng, &ctx->ids, &ctx->probs, &ctx->kept})
+  for (DevBuf* b : {&ctx->scratch, &ctx->params, &ctx->zeros, &ctx->slotmask, &ctx->status, &ctx->logits, &ctx->hist,
+                    &ctx->hoff, &ctx->allowed, &ctx->rng, &ctx->ids, &ctx->probs, &ctx->kept})
     b->release();
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -330,7 +356,16 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
   HIP_TRY(hipMemcpyAsync(rng_state, ctx->rng.ptr, B * sizeof(uint64_t), hipMemcpyDeviceToHost, s));
   if (out_kept) HIP_TRY(hipMemcpyAsync(out_kept, ctx->kept.ptr, B * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   if (out_probs) HIP_TRY(hipMemcpyAsync(out_probs, ctx->probs.ptr, nlog * sizeof(float), hipMemcpyDeviceToHost, s));
+  uint32_t kstatus = 0;
+  HIP_TRY(hipMemcpyAsync(&kstatus, ctx->status.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
+  if (kstatus) {
+    // A kernel hit an internal limit (its results are not trustworthy):
+    // report it and clear the word for the next call.
+    (void)hipMemset(ctx->status.ptr, 0, sizeof(uint32_t));
+    g_last_error = "internal error: a workgroup sync wait timed out in the sampler kernel";
+    return LLMHIP_ERR_HIP;
+  }
   return LLMHIP_OK;
 }
 
