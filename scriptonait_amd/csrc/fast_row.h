@@ -74,7 +74,7 @@ struct GenLds {
 };
 
 constexpr uint32_t kFastCand = 2048;              // candidates per row
-constexpr uint32_t kRegion = kFastCand / kWaves;  // raw hits per wave
+constexpr uint32_t kEntries = 64;                 // scan entries per wave
 constexpr uint32_t kHistPerThread = 2;            // history ids fetched per thread up front
 constexpr uint32_t kCoarseBins = 256;             // key bits 31..24
 constexpr uint32_t kFineBins = 4096;              // key bits 31..20
@@ -97,8 +97,8 @@ struct FastLds {
   uint32_t pm[kBlock];  // per-thread mask: slot is penalized
   __attribute__((aligned(16))) uint32_t coarse[kCoarseBins];
   __attribute__((aligned(16))) uint32_t fine[kFineBins];
-  uint32_t rv[kFastCand];    // raw hit value bits, per-wave regions
-  uint32_t rpos[kFastCand];  // raw hit position | slot << 24
+  float4 ent[kWaves * kEntries];     // scan entries: a lane's 4 values of a chunk with a hit
+  uint32_t etag[kWaves * kEntries];  // chunk position | hit mask << 24 | chunk << 28
   uint64_t ord[kFastCand];   // settled order keys
   uint32_t skey[kMaxFastK];  // sorted top-K: post-temperature key
   uint32_t sid[kMaxFastK];   //               id
@@ -298,10 +298,11 @@ __device__ __forceinline__ uint32_t lower_past_ties(uint32_t tau, float T, uint3
 
 // Ranks of the n candidates in ord[] (order keys, all distinct): rank(i) =
 // #{j : ord_j > ord_i}; the K best are written to skey/sid in sorted order.
-// All 16 waves share the candidates; each wave holds the whole list in
-// registers (NR keys per lane) and ranks an even slice of it, one ballot
-// per held key. Lane i collects candidate i's rank, so the loop body
-// touches no LDS and waits on nothing.
+// All 16 waves share the candidates;
+// each wave holds the whole list in registers (NR keys per lane) and ranks
+// an even slice of it, two at a time, one ballot per held key. Lane i
+// collects candidate i's rank, so the loop body touches no LDS and waits on
+// nothing.
 template <int NR>
 __device__ __forceinline__ void rank_in_regs(const uint64_t* ord, uint32_t n, uint32_t K, uint32_t wave,
                                              uint32_t lane, uint32_t* skey, uint32_t* sid) {
@@ -315,12 +316,15 @@ __device__ __forceinline__ void rank_in_regs(const uint64_t* ord, uint32_t n, ui
   const uint32_t i0 = min(n, wave * per), cnt = min(n, i0 + per) - i0;
   const uint64_t mi = lane < cnt ? ord[i0 + lane] : 0ull;
   uint32_t myr = 0xffffffffu;
-  for (uint32_t i = 0; i < cnt; ++i) {
-    const uint64_t oi = readlane_u64(mi, i);
-    uint32_t r = 0u;
+  for (uint32_t i = 0; i < cnt; i += 2u) {
+    const uint64_t oa = readlane_u64(mi, i), ob = readlane_u64(mi, min(i + 1u, cnt - 1u));
+    uint32_t ra = 0u, rb = 0u;
 #pragma unroll
-    for (int t = 0; t < NR; ++t) r += (uint32_t)__popcll((unsigned long long)__ballot(oj[t] > oi));
-    myr = lane == i ? r : myr;
+    for (int t = 0; t < NR; ++t) {
+      ra += (uint32_t)__popcll((unsigned long long)__ballot(oj[t] > oa));
+      rb += (uint32_t)__popcll((unsigned long long)__ballot(oj[t] > ob));
+    }
+    myr = lane == i ? ra : lane == i + 1u ? rb : myr;
   }
   if (lane < cnt && myr < K) {
     skey[myr] = (uint32_t)(mi >> 32);
@@ -353,7 +357,6 @@ template <int NCH, bool VEC>
 __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   static_assert(NCH * 4 <= 32, "slot masks are 32 bits");
   constexpr int S = NCH >= 4 ? NCH / 4 : 1;  // sample chunks per wave
-  constexpr int D = NCH >= 2 ? 2 : 1;        // chunks in flight per wave
   typedef float f4v __attribute__((ext_vector_type(4)));
 
   // The grid is exactly B workgroups.
@@ -365,7 +368,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
 
   // Every global load below is issued unconditionally (positions past V and
   // absent inputs read a valid dummy address), so each wait in the compiled
-  // code names exactly the loads it needs.
+  // code names exactly the loads it needs. The first half of the row goes
+  // out at once, the history ids when their offsets (a scalar load) are
+  // back, then the second half: the memory queues stay full from the start
+  // and the history lands right behind the first half.
   const float* row = a.logits + (size_t)b * a.ld;
   float x[NCH * 4];
   auto load_chunk = [&](int c) __attribute__((always_inline)) {
@@ -381,8 +387,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       for (int j = 0; j < 4; ++j) x[4 * c + j] = __builtin_nontemporal_load(row + (base + j < V ? base + j : 0u));
     }
   };
+  constexpr int NB1 = NCH >= 2 ? NCH / 2 : 1;  // chunks issued before the sample is in
 #pragma unroll
-  for (int c = 0; c < D; ++c) load_chunk(c);
+  for (int c = 0; c < NB1; ++c) load_chunk(c);
   const uint32_t mkbits = a.slotmask[tid];  // masked-out slots (allowed mask), or 0
   __builtin_amdgcn_sched_barrier(0);
 
@@ -393,6 +400,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   }
   const llmhip_params P = load_params(a, b);
   const uint64_t rng0 = as_const(a.rng_state)[b];
+  const float T = P.temperature, rp = P.repetition_penalty;
+  const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
+  const bool use_pen = H > 0 && H < 65536u;
 
   // LDS set-up (the count table only when a history may be used).
   if (wave == 0 && lane < 32) L.exptab[lane] = exp2f_tab_lane(lane);
@@ -404,39 +414,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
   L.pm[tid] = 0u;
   if (tid < 16) L.misc[tid] = 0u;
+  // The uniform draw of this row, ahead of the tail (rng.rs:16-34).
+  uint64_t st_next = rng0;
+  const float u_draw = next_f32(st_next);
 
-  auto chunk_full = [&](int c) __attribute__((always_inline)) {
-    return (wave * NCH + (uint32_t)c + 1u) * 256u <= V;
-  };
-  auto slot_valid = [&](int e) __attribute__((always_inline)) {
-    return chunk_full(e >> 2) || chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3) < V;
-  };
-
-  // 1. Sample: chunks 0..S-1 as they land; chunk c+D goes out as chunk c
-  //    arrives.
-  float sm = -INFINITY;
-  static_for<0, S>([&](auto cc) __attribute__((always_inline)) {
-    constexpr int c = decltype(cc)::value;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sm = slot_valid(4 * c + j) ? fmaxf(sm, x[4 * c + j]) : sm;
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (c + D < NCH) load_chunk(c + D);
-    __builtin_amdgcn_sched_barrier(0);
-  });
-  lds_barrier();  // LDS tables are zeroed
-  LLMHIP_MARK(1);
-
-  const uint32_t cls = row_class(P, V);
-  if (!(cls & a.row_class_mask)) return true;
-  const float T = P.temperature, rp = P.repetition_penalty;
-  const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
-  if (H >= 65536u) return false;  // a u16 multiplicity could overflow
-  const bool use_pen = H > 0;
-  const bool greedy = cls == kClassGreedy;
-  const uint32_t K = P.top_k;  // 0 < K < V, K <= kMaxFastK unless greedy (row class)
-
-  // Every wave fetches a slice of the history ids (counted a little later,
-  // when they have landed).
+  // Every wave fetches a slice of the history ids; they land behind the
+  // first half of the row.
   uint32_t hid[kHistPerThread];
   {
     const uint32_t* hsrc = use_pen ? a.hist + h0 : a.slotmask;
@@ -449,14 +432,111 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. Sample maxima into the histogram; the last wave to arrive selects the
-  //    speculative threshold. Q scales the target kSpecScale*K to the sample.
-  if (!greedy && sm > -INFINITY) {  // NaN and -inf maxima are not counted
-    const uint32_t k = f2key(sm);
-    atomicAdd(&L.coarse[k >> 24], 1u);
-    atomicAdd(&L.fine[k >> 20], 1u);
+  // Positions past V (in the one chunk that straddles V, or in chunks
+  // wholly past it) become -inf before their first use: no value at or
+  // above a threshold, never a maximum. The test is uniform per wave.
+  auto prep = [&](int c) __attribute__((always_inline)) {
+    if ((wave * NCH + (uint32_t)c + 1u) * 256u > V) {
+      const uint32_t base = chunk_pos<NCH>((uint32_t)c, wave, lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * c + j] = base + j < V ? x[4 * c + j] : -INFINITY;
+    }
+  };
+
+  const uint32_t cls = row_class(P, V);
+  if (!(cls & a.row_class_mask)) return true;
+  if (H >= 65536u) return false;  // a u16 multiplicity could overflow
+  const bool greedy = cls == kClassGreedy;
+  // A penalty below 1 (or NaN) can raise a value above the raw one, so the
+  // selection on raw values below does not bound such rows.
+  if (!greedy && use_pen && !(rp >= 1.0f)) return false;
+  const uint32_t K = P.top_k;  // 0 < K < V, K <= kMaxFastK unless greedy (row class)
+  lds_barrier();  // LDS tables are zeroed (no wave waits on its loads before this)
+  LLMHIP_MARK(1);
+
+  auto count_of = [&](uint32_t p) __attribute__((always_inline)) {
+    return (L.cnt[p >> 1] >> ((p & 1u) << 4)) & 0xffffu;
+  };
+  auto add_hist = [&](uint32_t id) __attribute__((always_inline)) {
+    if (id < V) {
+      const uint32_t sh = (id & 1u) << 4;
+      const uint32_t old = atomicAdd(&L.cnt[id >> 1], 1u << sh);
+      if (((old >> sh) & 0xffffu) == 0u) atomicOr(&L.pm[pos_owner<NCH>(id)], 1u << pos_slot<NCH>(id));
+    }
+  };
+  // History multiplicities (integer LDS atomics: the counts do not depend on
+  // the order). The first occurrence of an id marks its slot in the owner
+  // thread's mask.
+  auto count_history = [&]() __attribute__((always_inline)) {
+    if (use_pen) {
+#pragma unroll
+      for (uint32_t u = 0; u < kHistPerThread; ++u)
+        if (tid + u * kBlock < H) add_hist(hid[u]);
+      for (uint32_t j = tid + kHistPerThread * kBlock; j < H; j += kBlock) add_hist(a.hist[h0 + j]);
+    }
+    lds_signal(&L.misc[kSyncHist]);
+  };
+  // Mask and penalty of this thread's slot e, in the reference's order.
+  auto fix_value = [&](float v, int e, uint32_t pmv) __attribute__((always_inline)) {
+    if ((mkbits >> e) & 1u) v = -INFINITY;
+    if ((pmv >> e) & 1u) v = apply_penalty(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3)), rp);
+    return v;
+  };
+  auto fix_all = [&](uint32_t pmv) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if ((((pmv | mkbits) >> (4 * c)) & 0xfu) != 0u) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[4 * c + j] = fix_value(x[4 * c + j], 4 * c + j, pmv);
+      }
+    }
+  };
+
+  if (greedy) {
+    // ops/loss.rs:6-16 over the masked, penalized row (before temperature).
+#pragma unroll
+    for (int c = NB1; c < NCH; ++c) load_chunk(c);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) prep(c);
+    count_history();
+    uint32_t pmv = 0u;
+    if (use_pen) {
+      lds_wait(&L.misc[kSyncHist], kWaves, a.status);
+      pmv = L.pm[tid];
+    }
+    fix_all(pmv);
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+#pragma unroll
+    for (int e = 0; e < NCH * 4; ++e) {
+      if (x[e] > bv) {
+        bv = x[e];
+        bi = chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3);
+      }
+    }
+    const uint32_t w = block_argmax(bv, bi, L.redv, L.redi);
+    if (tid == 0) {
+      a.out_ids[b] = w == 0xffffffffu ? 0u : w;
+      if (a.out_kept) a.out_kept[b] = 0u;
+    }
+    return true;
   }
-  if (lds_signal(&L.misc[kSyncSample]) == kWaves - 1u && !greedy) {
+  // 1-2. Sample: per-thread maximum of chunks 0..S-1 (the first to land)
+  //    into the histogram; the last wave to arrive selects the speculative
+  //    threshold. Q scales the target kSpecScale*K to the sample.
+  {
+    float sm = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < S; ++c) prep(c);
+#pragma unroll
+    for (int e = 0; e < 4 * S; ++e) sm = fmaxf(sm, x[e]);
+    if (sm > -INFINITY) {  // NaN and -inf maxima are not counted
+      const uint32_t k = f2key(sm);
+      atomicAdd(&L.coarse[k >> 24], 1u);
+      atomicAdd(&L.fine[k >> 20], 1u);
+    }
+  }
+  if (lds_signal(&L.misc[kSyncSample]) == kWaves - 1u) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     LLMHIP_MARK(3);
     const bool whole = S == NCH;
@@ -470,186 +550,99 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
   }
   LLMHIP_MARK(2);
-
-  auto count_of = [&](uint32_t p) __attribute__((always_inline)) {
-    return (L.cnt[p >> 1] >> ((p & 1u) << 4)) & 0xffffu;
-  };
-  auto add_hist = [&](uint32_t id) __attribute__((always_inline)) {
-    if (id < V) {
-      const uint32_t sh = (id & 1u) << 4;
-      const uint32_t old = atomicAdd(&L.cnt[id >> 1], 1u << sh);
-      if (((old >> sh) & 0xffffu) == 0u) atomicOr(&L.pm[pos_owner<NCH>(id)], 1u << pos_slot<NCH>(id));
-    }
-  };
-  // Mask and penalty of this thread's slot e, in the reference's order.
-  auto fix_value = [&](float v, int e, uint32_t pmv) __attribute__((always_inline)) {
-    if ((mkbits >> e) & 1u) v = -INFINITY;
-    if ((pmv >> e) & 1u) v = apply_penalty(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3)), rp);
-    return v;
-  };
-  auto fix_chunk = [&](int c, uint32_t pmv) __attribute__((always_inline)) {
-    if ((((pmv | mkbits) >> (4 * c)) & 0xfu) != 0u) {
+  // The second half of the row, then the history counts (the ids landed
+  // with the first half).
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[4 * c + j] = fix_value(x[4 * c + j], 4 * c + j, pmv);
-    }
-  };
+  for (int c = NB1; c < NCH; ++c) load_chunk(c);
+  __builtin_amdgcn_sched_barrier(0);
+  count_history();
 
-  // Modes of a scan: kRaw compares raw values (hits are settled with mask
-  // and penalty afterwards); kFixFirst fixes every slot before its compare
-  // (a penalty p < 1 can raise a value); kFinal compares final values.
-  enum { kRaw = 0, kFixFirst = 1, kFinal = 2 };
-  const int mode0 = (use_pen && !(rp >= 1.0f)) ? kFixFirst : kRaw;
-  uint32_t pmv = 0u;
-  float tf = 0.0f;
-  uint32_t hits = 0u;  // this wave's raw hits so far
-  // Hits of chunk c: one compare per logit; for the rare chunks where some
-  // lane hits, a ballot offset and two LDS writes into the wave's region.
-  auto scan_chunk = [&](int c, int mode) __attribute__((always_inline)) {
-    if (mode == kFixFirst) fix_chunk(c, pmv);
+  // 4. The scan: every chunk against the published threshold, in landing
+  //    order (the compiler waits for each chunk at its first use). A lane
+  //    with a hit among its 4 values of a chunk appends one entry (the 4
+  //    values, the chunk's position and a 4-bit hit mask) to the wave's
+  //    region: one compare per value, and for the rare chunks where some
+  //    lane hits, one ballot offset and two LDS writes.
+  lds_wait(&L.misc[kTauState], 1u, a.status);
+  const uint32_t tau = lds_peek(&L.misc[kTauState]);
+  if (tau != 1u) return false;  // every wave read the same published state
+  float tf = key2f(L.misc[kTauKey]);
+  LLMHIP_MARK(4);
+  uint32_t nent = 0u;  // this wave's entries
+  auto scan_chunk = [&](int c) __attribute__((always_inline)) {
     const uint32_t base = chunk_pos<NCH>((uint32_t)c, wave, lane);
-    bool hit[4];
-    bool any = false;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      hit[j] = x[4 * c + j] >= tf;
-      if (!chunk_full(c)) hit[j] = hit[j] && base + j < V;
-      any = any || hit[j];
-    }
-    if (__ballot(any)) {
-      uint32_t* rvw = L.rv + wave * kRegion;
-      uint32_t* rpw = L.rpos + wave * kRegion;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint64_t m = __ballot(hit[j]);
-        const uint32_t o = hits + lanes_below(m);
-        if (hit[j] && o < kRegion) {
-          rvw[o] = __float_as_uint(x[4 * c + j]);
-          rpw[o] = (base + j) | ((uint32_t)(4 * c + j) << 24);
-        }
-        hits += (uint32_t)__popcll((unsigned long long)m);
+    const uint32_t hm = (x[4 * c] >= tf ? 1u : 0u) | (x[4 * c + 1] >= tf ? 2u : 0u) |
+                        (x[4 * c + 2] >= tf ? 4u : 0u) | (x[4 * c + 3] >= tf ? 8u : 0u);
+    const uint64_t m = __ballot(hm != 0u);
+    if (m) {
+      const uint32_t o = nent + lanes_below(m);
+      if (hm && o < kEntries) {
+        L.ent[wave * kEntries + o] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
+        L.etag[wave * kEntries + o] = base | (hm << 24) | ((uint32_t)c << 28);
       }
+      nent += (uint32_t)__popcll((unsigned long long)m);
     }
   };
-  // Settle this wave's hits: mask, penalty (kRaw only), recheck, and the
-  // post-temperature order key (one division, generate.rs:357-359), appended
-  // to ord[] with one LDS atomic per 64 hits.
-  auto settle = [&](int mode) __attribute__((always_inline)) {
-    if (hits > kRegion) {
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (c >= S) prep(c);
+    scan_chunk(c);
+  }
+  LLMHIP_MARK(5);
+
+  // 5. Settle this wave's entries: each lane takes an entry and handles its
+  //    hits one at a time (almost always one): mask, penalty, recheck
+  //    (final == false), then the post-temperature order key (one
+  //    division, generate.rs:357-359), appended to ord[] with one LDS
+  //    atomic per round.
+  uint32_t pmv = 0u;
+  auto settle = [&](bool final) __attribute__((always_inline)) {
+    if (nent > kEntries) {
       if (lane == 0) atomicOr(&L.misc[kOverflow], 1u);
       return;
     }
-    const uint32_t* rvw = L.rv + wave * kRegion;
-    const uint32_t* rpw = L.rpos + wave * kRegion;
-    for (uint32_t k0 = 0; k0 < hits; k0 += 64u) {
+    for (uint32_t k0 = 0; k0 < nent; k0 += 64u) {
       const uint32_t k = k0 + lane;
-      bool ok = k < hits;
-      const uint32_t tag = ok ? rpw[k] : 0u;
-      float v = ok ? __uint_as_float(rvw[k]) : 0.0f;
-      const uint32_t pos = tag & 0x00ffffffu;
-      if (mode == kRaw) {
-        // The hit's owner is a lane of this wave: fetch its mask word.
-        const uint32_t e = tag >> 24;
-        const uint32_t owner = pos_owner<NCH>(pos);
-        const uint32_t mkown = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((owner & 63u) << 2), (int)mkbits);
-        if (ok) {
+      float4 ev = make_float4(0.f, 0.f, 0.f, 0.f);
+      uint32_t tag = 0u;
+      if (k < nent) {
+        ev = L.ent[wave * kEntries + k];
+        tag = L.etag[wave * kEntries + k];
+      }
+      const uint32_t base = tag & 0x00ffffffu, c = tag >> 28;
+      uint32_t rem = (tag >> 24) & 0xfu;
+      // The entry's owner is a lane of this wave: fetch its mask words.
+      const uint32_t owner = pos_owner<NCH>(base);
+      const uint32_t mkown = final ? 0u : (uint32_t)__builtin_amdgcn_ds_bpermute((int)((owner & 63u) << 2), (int)mkbits);
+      const uint32_t pmown = (final || !use_pen || k >= nent) ? 0u : L.pm[owner];
+      while (__ballot(rem != 0u)) {
+        // A lane takes part in a round only while it has a hit left.
+        bool ok = rem != 0u;
+        const uint32_t j = ok ? (uint32_t)__builtin_ctz(rem) : 0u;
+        rem &= rem - 1u;
+        float v = j == 0 ? ev.x : j == 1 ? ev.y : j == 2 ? ev.z : ev.w;
+        const uint32_t e = 4u * c + j, pos = base + j;
+        if (ok && !final) {
           if ((mkown >> e) & 1u) v = -INFINITY;
-          if (use_pen && ((L.pm[owner] >> e) & 1u)) v = apply_penalty(v, count_of(pos), rp);
+          if ((pmown >> e) & 1u) v = apply_penalty(v, count_of(pos), rp);
           ok = v >= tf;
         }
-      }
-      const uint64_t mk = __ballot(ok);
-      if (mk) {
-        uint32_t o = 0u;
-        if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
-        o = readlane_u32(o, 0) + lanes_below(mk);
-        if (ok && o < kFastCand) L.ord[o] = cand_order(f2key(v / T), pos);
+        const uint64_t mk = __ballot(ok);
+        if (mk) {
+          uint32_t o = 0u;
+          if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
+          o = readlane_u32(o, 0) + lanes_below(mk);
+          if (ok && o < kFastCand) L.ord[o] = cand_order(f2key(v / T), pos);
+        }
       }
     }
   };
-
-  // 3-4. History counts, then the scan of every chunk as soon as both it
-  //    and the threshold are there. Step c runs when chunk c has landed
-  //    (the compiler waits for it at its first use); step NCH closes.
-  constexpr int CH = S + 1 < NCH ? S + 1 : NCH;  // step that counts the history
-  uint32_t scanned = 0u;  // chunks scanned so far
-  uint32_t tau = 0u;      // 0: not yet, 1: threshold in tf, 2: not bounded
-  static_for<S, NCH + 1>([&](auto cc) __attribute__((always_inline)) {
-    constexpr int c = decltype(cc)::value;
-    if constexpr (c < NCH) {
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (c + D < NCH) load_chunk(c + D);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (c == CH) {
-      // History multiplicities (the ids have landed by now). The first
-      // occurrence of an id marks its slot in the owner thread's mask.
-      if (use_pen) {
-#pragma unroll
-        for (uint32_t u = 0; u < kHistPerThread; ++u)
-          if (tid + u * kBlock < H) add_hist(hid[u]);
-        for (uint32_t j = tid + kHistPerThread * kBlock; j < H; j += kBlock) add_hist(a.hist[h0 + j]);
-      }
-      lds_signal(&L.misc[kSyncHist]);
-    }
-    if (greedy || tau == 2u) return;
-    if (tau == 0u) {
-      // kFixFirst waits below for every wave's history counts, so it may
-      // start only once this wave has counted its own (step CH).
-      if (mode0 == kFixFirst && c < CH) return;
-      if constexpr (c == NCH) lds_wait(&L.misc[kTauState], 1u, a.status);
-      tau = lds_peek(&L.misc[kTauState]);
-      if (tau != 1u) return;  // not published yet (scan later), or not bounded
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-      tf = key2f(L.misc[kTauKey]);
-      if (mode0 == kFixFirst) {
-        lds_wait(&L.misc[kSyncHist], kWaves, a.status);
-        pmv = L.pm[tid];
-      }
-      LLMHIP_MARK(4);
-    }
-    // Chunks scanned..min(c, NCH-1) have landed: scan them.
-    static_for<0, (c < NCH ? c + 1 : NCH)>([&](auto qq) __attribute__((always_inline)) {
-      constexpr int q = decltype(qq)::value;
-      if (scanned <= (uint32_t)q) scan_chunk(q, mode0);
-    });
-    scanned = c < NCH ? c + 1 : NCH;
-  });
-  LLMHIP_MARK(5);
-
-  if (greedy) {
-    // ops/loss.rs:6-16 over the masked, penalized row (before temperature).
-    if (use_pen) {
-      lds_wait(&L.misc[kSyncHist], kWaves, a.status);
-      pmv = L.pm[tid];
-    }
-    float bv = -INFINITY;
-    uint32_t bi = 0xffffffffu;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      fix_chunk(c, pmv);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = 4 * c + j;
-        if (x[e] > bv && slot_valid(e)) {
-          bv = x[e];
-          bi = chunk_pos<NCH>((uint32_t)c, wave, lane) + j;
-        }
-      }
-    }
-    const uint32_t w = block_argmax(bv, bi, L.redv, L.redi);
-    if (tid == 0) {
-      a.out_ids[b] = w == 0xffffffffu ? 0u : w;
-      if (a.out_kept) a.out_kept[b] = 0u;
-    }
-    return true;
-  }
-  if (tau == 2u) return false;  // every wave read the same state
-
-  if (use_pen && mode0 == kRaw) {
+  if (use_pen) {
     lds_wait(&L.misc[kSyncHist], kWaves, a.status);
     pmv = L.pm[tid];
   }
-  settle(mode0);
+  settle(false);
   lds_barrier();
   LLMHIP_MARK(6);
   uint32_t n = L.misc[kCandN];
@@ -661,13 +654,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     // the masked, penalized row (at least K values lie at or above it, in
     // the threads whose maximum does). Everyone is past the sample
     // histogram, so it is reused.
+    fix_all(pmv);
     float tm = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (mode0 == kRaw) fix_chunk(c, pmv);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) tm = slot_valid(4 * c + j) ? fmaxf(tm, x[4 * c + j]) : tm;
-    }
+    for (int e = 0; e < NCH * 4; ++e) tm = fmaxf(tm, x[e]);
     reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid == 0) {
@@ -685,10 +675,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     if (tkey == 0u) return false;
     tf = key2f(tkey);
     // Values are final now (fixed in place).
-    hits = 0u;
+    nent = 0u;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) scan_chunk(c, kFinal);
-    settle(kFinal);
+    for (int c = 0; c < NCH; ++c) scan_chunk(c);
+    settle(true);
     lds_barrier();
     n = L.misc[kCandN];
     // Heavy ties or an unusually flat top: not bounded by the register path.
@@ -699,6 +689,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   LLMHIP_MARK(9);
   if (n <= 128) {
     rank_in_regs<2>(L.ord, n, K, wave, lane, L.skey, L.sid);
+  } else if (n <= 192) {
+    rank_in_regs<3>(L.ord, n, K, wave, lane, L.skey, L.sid);
   } else if (n <= 256) {
     rank_in_regs<4>(L.ord, n, K, wave, lane, L.skey, L.sid);
   } else if (n <= 512) {
@@ -713,8 +705,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // 7. The sequential tail (one wave).
   if (wave == 0) {
     if (K <= 64) {
-      draw_tail_small(a, b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u, rng0,
-                      L.tail, L.exptab);
+      draw_tail_bcast(a, b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u, u_draw,
+                      st_next, L.exptab, L.tail);
     } else {
       draw_tail(a, b, P, K, [&](uint32_t i) { return L.skey[i]; }, [&](uint32_t i) { return L.sid[i]; }, rng0,
                 L.exptab);
