@@ -391,7 +391,9 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
     return (i & 3) == 0 ? f.x : (i & 3) == 1 ? f.y : (i & 3) == 2 ? f.z : f.w;
   };
 
-  // generate.rs:374: sum = ((0 + e_0) + e_1) + ... over the n terms.
+  // generate.rs:374: sum = ((0 + e_0) + e_1) + ... over the n terms, as 64
+  // dependent adds: the terms past n are +0, which leave a sum >= e_0 = 1
+  // (or a NaN one) unchanged.
   buf[lane] = e;
   float sum = 0.0f;
   {
@@ -399,11 +401,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
 #pragma unroll
     for (int q = 0; q < 16; ++q) w[q] = b4[q];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (8u * k >= n) break;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sum += term(w, 8 * k + j);
-    }
+    for (int i = 0; i < 64; ++i) sum += term(w, i);
   }
   // generate.rs:375-377: degenerate exit, no draw.
   if (!(sum > 0.0f) || !isfinite(sum)) {
@@ -431,62 +429,60 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
 
   // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; top-p keeps up to the
   // first c_i >= top_p (all when top_p >= 1 or never reached); the total
-  // over the kept prefix is the fold at its last element.
+  // over the kept prefix is the fold at its last element. The fold runs in
+  // blocks of 8 dependent adds; c never decreases (p_i >= 0), so only the
+  // last value of a block is tested, and the block that holds the stop (or
+  // the end of the kept prefix) is resolved once, after the loop: lane
+  // 8k+j takes c_{8k+j} and one ballot finds the first c_i >= top_p.
   const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
   uint32_t stop = keep;
-  float total = 0.0f;
+  float total;
   {
-    float c = 0.0f;
+    float c = 0.0f, cb[8];
+    uint32_t k = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      float cb[8];
+    for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        c += term(pv, 8 * k + j);
+        c += term(pv, 8 * kk + j);
         cb[j] = c;
       }
-      // Steps 8k .. 8k+7; only those below keep count.
-      const uint32_t lim = keep - 8u * k;  // >= 1 here
-      if (c >= tp || lim <= 8u) {
-        uint32_t jj = lim < 8u ? lim - 1u : 7u;  // last counted step
-#pragma unroll
-        for (int j = 7; j >= 0; --j)
-          if ((uint32_t)j < lim && cb[j] >= tp) jj = (uint32_t)j;
-        const bool hit = cb[jj] >= tp;
-        stop = hit ? 8u * k + jj + 1u : keep;
-        float t = cb[0];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) t = (uint32_t)j == stop - 1u - 8u * k ? cb[j] : t;
-        total = t;
-        break;
-      }
+      k = (uint32_t)kk;
+      if (c >= tp || 8u * (uint32_t)(kk + 1) >= keep) break;
     }
+    const uint32_t k8 = 8u * k;
+    float t = cb[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) t = lane == k8 + (uint32_t)j ? cb[j] : t;
+    const uint64_t hit = __ballot(lane >= k8 && lane < k8 + 8u && lane < keep && t >= tp);
+    if (hit) stop = (uint32_t)__ffsll((unsigned long long)hit);
+    total = readlane_f32(t, stop - 1u);
   }
 
   // generate.rs:412-419: r_0 = u * total; step i tests r_i < p_i and then
-  // subtracts p_i. r - p < 0 exactly when r < p, so a block with a pick ends
-  // negative.
+  // subtracts p_i. r - p < 0 exactly when r < p (f32 denormals are kept), so
+  // the block holding the pick is the first that ends negative; lane 8k+j
+  // takes r_{8k+j} and compares it with its own p.
   uint32_t pick = stop - 1u;
   {
-    float r = u * total;
+    float r = u * total, rb[8];
+    uint32_t k = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      float rb[8];
+    for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         rb[j] = r;
-        r -= term(pv, 8 * k + j);
+        r -= term(pv, 8 * kk + j);
       }
-      const uint32_t lim = stop - 8u * k;
-      if (r < 0.0f || lim <= 8u) {
-        uint32_t jj = 8u;
-#pragma unroll
-        for (int j = 7; j >= 0; --j)
-          if ((uint32_t)j < lim && rb[j] < term(pv, 8 * k + j)) jj = (uint32_t)j;
-        if (jj < 8u) pick = 8u * k + jj;
-        break;
-      }
+      k = (uint32_t)kk;
+      if (r < 0.0f || 8u * (uint32_t)(kk + 1) >= stop) break;
     }
+    const uint32_t k8 = 8u * k;
+    float t = rb[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) t = lane == k8 + (uint32_t)j ? rb[j] : t;
+    const uint64_t hit = __ballot(lane >= k8 && lane < k8 + 8u && lane < stop && t < p);
+    if (hit) pick = (uint32_t)__ffsll((unsigned long long)hit) - 1u;
   }
   const uint32_t id = readlane_u32(my_id, pick);
   if (lane == 0) {

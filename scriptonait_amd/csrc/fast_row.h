@@ -2,48 +2,38 @@
 // V <= 32768, 0 < top_k <= 1024 (and greedy rows).
 //
 // Row semantics: crates/llm-core/src/generate.rs:325-420. The row is read
-// once from HBM into registers; the work that decides the sample runs while
-// the row streams in, and only a compare, one settle pass, two workgroup
-// barriers, a rank over ~2K candidates and the sequential tail remain after
-// the last byte lands.
+// once from HBM into registers, all of it at once (the memory queues run
+// full from the first cycle), and the selection threshold is taken from the
+// waves whose data lands first, so only a compare, one settle pass, two
+// workgroup barriers, a rank over ~1.5K candidates and the sequential tail
+// remain after the last byte lands.
 //
-// Layout. Wave w owns the contiguous 1 KiB blocks w*NCH .. w*NCH+NCH-1 of
-// the row (256 floats each); lane l of wave w holds block (w*NCH + c)'s
-// floats 4l..4l+3 as its chunk c, loaded with one nontemporal dwordx4. Every
-// load is 1 KiB contiguous per wave, and the first S chunks of all waves
-// form a sample spread evenly over the whole row.
-//
-// Streaming. A wave keeps D chunks in flight: chunk c+D is issued when chunk
-// c has landed. That keeps the HBM queues as full as issuing everything at
-// once would, but the chunks land in order, so the sample is complete early
-// and the scan keeps pace with the data.
-//
-// Throughput. The 16 waves of a workgroup share one CU: one scalar unit and
-// four SIMDs. Work that every wave would repeat (the threshold) is done by
-// one wave, and per-chunk work is a compare and a rare append.
+// Layout. Lane l of wave w holds chunk c = floats 4l..4l+3 of the 1 KiB
+// block c*16 + w of the row, loaded with one nontemporal dwordx4: every
+// load is 1 KiB contiguous per wave, and the blocks of any set of waves are
+// spread evenly over the whole row.
 //
 // Per wave:
-//  1. chunks 0..S-1 land: per-thread maximum of the sample.
-//  2. LDS barrier (tables zeroed); the maxima go into a two-level key
-//     histogram; the wave signals. The wave that signals last selects the
-//     speculative threshold (about 2K of the row's values expected at or
-//     above it) and publishes it in LDS.
-//  3. history ids are counted: u16 multiplicities and per-owner masks of
+//  1. the row lands: per-chunk and per-thread maxima.
+//  2. the first 12 waves to get here put their per-thread maxima in a
+//     two-level key histogram; the 12th selects the threshold (about 1.5K
+//     of the row's values expected at or above it, scaled from the 3/4 of
+//     the row those waves hold) and publishes it in LDS.
+//  3. each chunk whose maximum reaches the threshold is compared value by
+//     value; hits go to the wave's LDS region.
+//  4. history ids are counted: u16 multiplicities and per-owner masks of
 //     penalized slots, integer LDS atomics whose result does not depend on
 //     order.
-//  4. each landed chunk is compared with the threshold once it is published
-//     (chunks that landed before are caught up); hits go to the wave's LDS
-//     region.
-//  5. after the last chunk, the wave settles its hits (mask, penalty m times
-//     in sequence, recheck, one division by T) into the candidate list.
+//  5. the wave settles its hits (mask, penalty m times in sequence,
+//     recheck, one division by T) into the candidate list.
 //  6. barrier; the count check (>= K proves the threshold); rank; barrier.
 //  7. one wave replays the reference's folds and draws.
 //
 // Selecting on raw values is exact: the mask sets -inf and a penalty
 // p >= 1 never raises a value (l/p <= l for l > 0, l*p <= l for l <= 0,
 // each correctly rounded), so every value at or above the threshold after
-// mask and penalty was at or above it before. For p < 1 (or NaN) the values
-// are fixed up before the compare instead.
+// mask and penalty was at or above it before. Rows with p < 1 (or NaN) take
+// the general path.
 #pragma once
 #include <type_traits>
 
@@ -75,10 +65,11 @@ struct GenLds {
 
 constexpr uint32_t kFastCand = 2048;              // candidates per row
 constexpr uint32_t kEntries = 64;                 // scan entries per wave
-constexpr uint32_t kHistPerThread = 2;            // history ids fetched per thread up front
+constexpr uint32_t kHistPerThread = 1;            // history ids fetched per thread with the row
 constexpr uint32_t kCoarseBins = 256;             // key bits 31..24
 constexpr uint32_t kFineBins = 4096;              // key bits 31..20
-constexpr uint32_t kSpecScale = 2;                // speculative threshold aims at ~kSpecScale*K values
+constexpr uint32_t kTauWaves = 8;                 // waves whose maxima form the threshold sample
+constexpr uint32_t kSpecNum = 8, kSpecDen = 5;    // the threshold aims at ~(kSpecNum/kSpecDen)*K values
 
 // misc[] slots
 constexpr int kSyncSample = 0;  // waves whose sample is in the histogram
@@ -87,6 +78,9 @@ constexpr int kCandN = 2;       // candidates in ord[]
 constexpr int kOverflow = 3;    // some wave's region overflowed
 constexpr int kTauState = 4;    // 0: not yet, 1: published in kTauKey, 2: row not bounded here
 constexpr int kTauKey = 5;
+constexpr int kArrive = 6;   // waves whose row has landed, in arrival order
+constexpr int kSampled = 7;  // row positions held by the sample waves
+constexpr int kSyncZero = 8; // waves whose share of the count table is zeroed
 
 template <int NCH>
 struct FastLds {
@@ -199,18 +193,38 @@ __device__ __forceinline__ void lds_wait(const uint32_t* ctr, uint32_t target, u
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+#ifndef LLMHIP_STRIDED
+#define LLMHIP_STRIDED 1
+#endif
+// Block (1 KiB, 256 floats) that wave `wave` holds as its chunk c.
+template <int NCH>
+__device__ __forceinline__ uint32_t chunk_block(uint32_t c, uint32_t wave) {
+  return LLMHIP_STRIDED ? c * kWaves + wave : wave * NCH + c;
+}
 // Row position of chunk c's first float in lane `lane` of wave `wave`.
 template <int NCH>
 __device__ __forceinline__ uint32_t chunk_pos(uint32_t c, uint32_t wave, uint32_t lane) {
-  return ((wave * NCH + c) * 64u + lane) * 4u;
+  return (chunk_block<NCH>(c, wave) * 64u + lane) * 4u;
 }
+// Thread (wave*64 + lane) and slot (4*chunk + j) holding row position p.
 template <int NCH>
 __device__ __forceinline__ uint32_t pos_owner(uint32_t p) {
-  return ((p >> 8) / NCH) * 64u + ((p >> 2) & 63u);
+  return (LLMHIP_STRIDED ? (p >> 8) % kWaves : (p >> 8) / NCH) * 64u + ((p >> 2) & 63u);
 }
 template <int NCH>
 __device__ __forceinline__ uint32_t pos_slot(uint32_t p) {
-  return ((p >> 8) % NCH) * 4u + (p & 3u);
+  return (LLMHIP_STRIDED ? (p >> 8) / kWaves : (p >> 8) % NCH) * 4u + (p & 3u);
+}
+// Row positions (< V) held by wave `wave`.
+template <int NTOT, int NCH>
+__device__ __forceinline__ uint32_t wave_positions(uint32_t wave, uint32_t V) {
+  uint32_t n = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const uint32_t s0 = chunk_block<NTOT>((uint32_t)c, wave) * 256u;
+    n += s0 >= V ? 0u : min(256u, V - s0);
+  }
+  return n;
 }
 
 // Candidate order key: larger = earlier in the reference's sort (value
@@ -356,7 +370,6 @@ __device__ __forceinline__ void rank_in_lds(const uint64_t* ord, uint32_t n, uin
 template <int NCH, bool VEC>
 __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   static_assert(NCH * 4 <= 32, "slot masks are 32 bits");
-  constexpr int S = NCH >= 4 ? NCH / 4 : 1;  // sample chunks per wave
   typedef float f4v __attribute__((ext_vector_type(4)));
 
   // The grid is exactly B workgroups.
@@ -364,14 +377,38 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
   const uint32_t V = a.V;
+  // The kernel arguments this path reads, fetched here in one batch (left
+  // to itself the compiler fetches some at their first use, behind the
+  // row's loads, and the LDS barrier below would wait for them).
+  asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.params), "s"(a.params_stride), "s"(a.hist),
+               "s"(a.hist_offsets), "s"(a.slotmask), "s"(a.status), "s"(a.rng_state), "s"(a.out_ids),
+               "s"(a.out_probs), "s"(a.out_kept), "s"(a.row_class_mask));
+  asm volatile("" ::"s"(a.shared.temperature), "s"(a.shared.top_k), "s"(a.shared.top_p), "s"(a.shared.min_p),
+               "s"(a.shared.repetition_penalty), "s"(a.eos_id), "s"(a.allowed), "s"(a.allowed_len), "s"(a.B),
+               "s"(a.scratch), "s"(a.scratch_row_words));
   LLMHIP_MARK(0);
 
   // Every global load below is issued unconditionally (positions past V and
   // absent inputs read a valid dummy address), so each wait in the compiled
-  // code names exactly the loads it needs. The first half of the row goes
-  // out at once, the history ids when their offsets (a scalar load) are
-  // back, then the second half: the memory queues stay full from the start
-  // and the history lands right behind the first half.
+  // code names exactly the loads it needs. A wave's loads complete at a
+  // limited rate (a CU holds only part of its 128 KiB row in flight, and a
+  // wave stalls at a load until earlier data has returned), so every wave
+  // issues its part of the row as early as it can: the first two chunks,
+  // the LDS set-up and its barrier in their shadow, then the rest, then the
+  // history ids (their offsets are back by then).
+  //
+  // The row's scalars go out first, by vector loads (lane l reads word l),
+  // which count in order with the row's loads: a scalar load would share its
+  // counter with LDS operations, and every LDS wait before it returned
+  // (behind the row) would wait for it.
+  const bool has_hist = a.hist_offsets && a.hist;
+  const uint32_t hv = (has_hist ? a.hist_offsets + b : a.slotmask)[lane & 1u];
+  const uint32_t rv = reinterpret_cast<const uint32_t*>(a.rng_state + b)[lane & 1u];
+  const uint32_t pw =
+      a.params ? reinterpret_cast<const uint32_t*>(a.params + (size_t)b * a.params_stride)[min(lane, 4u)] : 0u;
+  const uint32_t mkbits = a.slotmask[tid];  // masked-out slots (allowed mask), or 0
+  __builtin_amdgcn_sched_barrier(0);
+
   const float* row = a.logits + (size_t)b * a.ld;
   float x[NCH * 4];
   auto load_chunk = [&](int c) __attribute__((always_inline)) {
@@ -387,56 +424,61 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       for (int j = 0; j < 4; ++j) x[4 * c + j] = __builtin_nontemporal_load(row + (base + j < V ? base + j : 0u));
     }
   };
-  constexpr int NB1 = NCH >= 2 ? NCH / 2 : 1;  // chunks issued before the sample is in
+  constexpr int NB0 = NCH >= 2 ? 2 : 1;
 #pragma unroll
-  for (int c = 0; c < NB1; ++c) load_chunk(c);
-  const uint32_t mkbits = a.slotmask[tid];  // masked-out slots (allowed mask), or 0
+  for (int c = 0; c < NB0; ++c) load_chunk(c);
   __builtin_amdgcn_sched_barrier(0);
 
-  uint32_t h0 = 0, h1 = 0;
-  if (a.hist_offsets && a.hist) {
-    h0 = as_const(a.hist_offsets)[b];
-    h1 = as_const(a.hist_offsets)[b + 1];
-  }
-  const llmhip_params P = load_params(a, b);
-  const uint64_t rng0 = as_const(a.rng_state)[b];
-  const float T = P.temperature, rp = P.repetition_penalty;
-  const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
-  const bool use_pen = H > 0 && H < 65536u;
-
-  // LDS set-up (the count table only when a history may be used).
+  // LDS set-up; every wave zeroes its share of the count table later.
   if (wave == 0 && lane < 32) L.exptab[lane] = exp2f_tab_lane(lane);
-  if (a.hist) {
-    uint4* c4 = reinterpret_cast<uint4*>(L.cnt);
-    for (uint32_t i = tid; i < (V + 7u) / 8u; i += kBlock) c4[i] = make_uint4(0u, 0u, 0u, 0u);
-  }
   reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);  // kFineBins / 4 == kBlock
   if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
   L.pm[tid] = 0u;
   if (tid < 16) L.misc[tid] = 0u;
-  // The uniform draw of this row, ahead of the tail (rng.rs:16-34).
-  uint64_t st_next = rng0;
-  const float u_draw = next_f32(st_next);
+  lds_barrier();  // LDS tables are zeroed
+  LLMHIP_MARK(1);
+#pragma unroll
+  for (int c = NB0; c < NCH; ++c) load_chunk(c);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // Every wave fetches a slice of the history ids; they land behind the
-  // first half of the row.
+  const uint32_t h0 = has_hist ? readlane_u32(hv, 0) : 0u, h1 = has_hist ? readlane_u32(hv, 1) : 0u;
+  const uint64_t rng0 = ((uint64_t)readlane_u32(rv, 1) << 32) | readlane_u32(rv, 0);
+  llmhip_params P = a.shared;
+  if (a.params) {
+    P.temperature = __uint_as_float(readlane_u32(pw, 0));
+    P.top_k = readlane_u32(pw, 1);
+    P.top_p = __uint_as_float(readlane_u32(pw, 2));
+    P.min_p = __uint_as_float(readlane_u32(pw, 3));
+    P.repetition_penalty = __uint_as_float(readlane_u32(pw, 4));
+  }
+  const float T = P.temperature, rp = P.repetition_penalty;
+  const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
+  const bool use_pen = H > 0 && H < 65536u;
+  // History ids: lane t of the workgroup fetches ids t, t+1024, ...; they
+  // land right behind the wave's part of the row.
   uint32_t hid[kHistPerThread];
   {
     const uint32_t* hsrc = use_pen ? a.hist + h0 : a.slotmask;
     const uint32_t hmax = use_pen ? H - 1u : 0u;
 #pragma unroll
-    for (uint32_t u = 0; u < kHistPerThread; ++u) {
-      const uint32_t j = tid + u * kBlock;
-      hid[u] = hsrc[j < hmax ? j : hmax];
-    }
+    for (uint32_t u = 0; u < kHistPerThread; ++u) hid[u] = hsrc[min(tid + u * kBlock, hmax)];
   }
   __builtin_amdgcn_sched_barrier(0);
+  // This wave's share of the count table (only when a history may be used).
+  if (a.hist) {
+    uint4* c4 = reinterpret_cast<uint4*>(L.cnt);
+    for (uint32_t i = tid; i < (V + 7u) / 8u; i += kBlock) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  lds_signal(&L.misc[kSyncZero]);
+  // The uniform draw of this row, ahead of the tail (rng.rs:16-34).
+  uint64_t st_next = rng0;
+  const float u_draw = next_f32(st_next);
 
   // Positions past V (in the one chunk that straddles V, or in chunks
   // wholly past it) become -inf before their first use: no value at or
   // above a threshold, never a maximum. The test is uniform per wave.
   auto prep = [&](int c) __attribute__((always_inline)) {
-    if ((wave * NCH + (uint32_t)c + 1u) * 256u > V) {
+    if ((chunk_block<NCH>((uint32_t)c, wave) + 1u) * 256u > V) {
       const uint32_t base = chunk_pos<NCH>((uint32_t)c, wave, lane);
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[4 * c + j] = base + j < V ? x[4 * c + j] : -INFINITY;
@@ -451,8 +493,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // selection on raw values below does not bound such rows.
   if (!greedy && use_pen && !(rp >= 1.0f)) return false;
   const uint32_t K = P.top_k;  // 0 < K < V, K <= kMaxFastK unless greedy (row class)
-  lds_barrier();  // LDS tables are zeroed (no wave waits on its loads before this)
-  LLMHIP_MARK(1);
 
   auto count_of = [&](uint32_t p) __attribute__((always_inline)) {
     return (L.cnt[p >> 1] >> ((p & 1u) << 4)) & 0xffffu;
@@ -469,6 +509,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // thread's mask.
   auto count_history = [&]() __attribute__((always_inline)) {
     if (use_pen) {
+      lds_wait(&L.misc[kSyncZero], kWaves, a.status);
 #pragma unroll
       for (uint32_t u = 0; u < kHistPerThread; ++u)
         if (tid + u * kBlock < H) add_hist(hid[u]);
@@ -495,8 +536,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   if (greedy) {
     // ops/loss.rs:6-16 over the masked, penalized row (before temperature).
 #pragma unroll
-    for (int c = NB1; c < NCH; ++c) load_chunk(c);
-#pragma unroll
     for (int c = 0; c < NCH; ++c) prep(c);
     count_history();
     uint32_t pmv = 0u;
@@ -521,74 +560,79 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
     return true;
   }
-  // 1-2. Sample: per-thread maximum of chunks 0..S-1 (the first to land)
-  //    into the histogram; the last wave to arrive selects the speculative
-  //    threshold. Q scales the target kSpecScale*K to the sample.
-  {
-    float sm = -INFINITY;
+  // 1. The row has landed: per-chunk and per-thread maxima (NaN is never a
+  //    maximum).
+  constexpr int NS = NCH;
+  auto max4 = [&](int c) __attribute__((always_inline)) {
+    return fmaxf(fmaxf(x[4 * c], x[4 * c + 1]), fmaxf(x[4 * c + 2], x[4 * c + 3]));
+  };
+  float mc[NCH];
+  float tm = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < S; ++c) prep(c);
-#pragma unroll
-    for (int e = 0; e < 4 * S; ++e) sm = fmaxf(sm, x[e]);
-    if (sm > -INFINITY) {  // NaN and -inf maxima are not counted
-      const uint32_t k = f2key(sm);
-      atomicAdd(&L.coarse[k >> 24], 1u);
-      atomicAdd(&L.fine[k >> 20], 1u);
-    }
-  }
-  if (lds_signal(&L.misc[kSyncSample]) == kWaves - 1u) {
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    LLMHIP_MARK(3);
-    const bool whole = S == NCH;
-    const uint32_t Q =
-        whole ? K : (uint32_t)(((uint64_t)kSpecScale * K * a.spec_sampled + V - 1u) / V) + 2u;
-    const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, Q, whole, lane), T, lane);
-    if (lane == 0) {
-      L.misc[kTauKey] = tkey;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-      __hip_atomic_store(&L.misc[kTauState], tkey ? 1u : 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
+  for (int c = 0; c < NS; ++c) {
+    prep(c);
+    mc[c] = max4(c);
+    tm = fmaxf(tm, mc[c]);
   }
   LLMHIP_MARK(2);
-  // The second half of the row, then the history counts (the ids landed
-  // with the first half).
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int c = NB1; c < NCH; ++c) load_chunk(c);
-  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. The first kTauWaves waves to get here put their sample maxima in the
+  //    histogram, and the last of them selects the speculative threshold:
+  //    the Q-th largest sampled maximum, with Q scaled from the target
+  //    (kSpecNum/kSpecDen)*K to the positions the sample holds.
+  {
+    uint32_t arrive = 0u;
+    if (lane == 0u) arrive = __hip_atomic_fetch_add(&L.misc[kArrive], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    arrive = readlane_u32(arrive, 0);
+    if (arrive < kTauWaves) {
+      if (tm > -INFINITY) {  // a NaN or -inf maximum is not counted
+        const uint32_t k = f2key(tm);
+        atomicAdd(&L.coarse[k >> 24], 1u);
+        atomicAdd(&L.fine[k >> 20], 1u);
+      }
+      if (lane == 0u) atomicAdd(&L.misc[kSampled], wave_positions<NCH, NS>(wave, V));
+      if (lds_signal(&L.misc[kSyncSample]) == kTauWaves - 1u) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        LLMHIP_MARK(3);
+        const uint64_t sampled = L.misc[kSampled];
+        const uint32_t Q =
+            (uint32_t)(((uint64_t)kSpecNum * K * sampled + (uint64_t)kSpecDen * V - 1u) / ((uint64_t)kSpecDen * V)) + 2u;
+        const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, Q, false, lane), T, lane);
+        if (lane == 0) {
+          L.misc[kTauKey] = tkey;
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+          __hip_atomic_store(&L.misc[kTauState], tkey ? 1u : 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+      }
+    }
+  }
+  // The history counts (the ids land right behind the wave's chunks).
   count_history();
 
-  // 4. The scan: every chunk against the published threshold, in landing
-  //    order (the compiler waits for each chunk at its first use). A lane
-  //    with a hit among its 4 values of a chunk appends one entry (the 4
-  //    values, the chunk's position and a 4-bit hit mask) to the wave's
-  //    region: one compare per value, and for the rare chunks where some
-  //    lane hits, one ballot offset and two LDS writes.
+  // 3. The scan: every lane whose maximum over a chunk reaches the
+  //    published threshold appends one entry (the chunk's 4 values and its
+  //    position) to the wave's region: one compare per chunk, and for the
+  //    chunks where some lane hits, one ballot offset and two LDS writes.
   lds_wait(&L.misc[kTauState], 1u, a.status);
   const uint32_t tau = lds_peek(&L.misc[kTauState]);
   if (tau != 1u) return false;  // every wave read the same published state
   float tf = key2f(L.misc[kTauKey]);
   LLMHIP_MARK(4);
   uint32_t nent = 0u;  // this wave's entries
-  auto scan_chunk = [&](int c) __attribute__((always_inline)) {
-    const uint32_t base = chunk_pos<NCH>((uint32_t)c, wave, lane);
-    const uint32_t hm = (x[4 * c] >= tf ? 1u : 0u) | (x[4 * c + 1] >= tf ? 2u : 0u) |
-                        (x[4 * c + 2] >= tf ? 4u : 0u) | (x[4 * c + 3] >= tf ? 8u : 0u);
-    const uint64_t m = __ballot(hm != 0u);
+  auto scan_chunk = [&](int c, float mcv) __attribute__((always_inline)) {
+    const bool hit = mcv >= tf;
+    const uint64_t m = __ballot(hit);
     if (m) {
       const uint32_t o = nent + lanes_below(m);
-      if (hm && o < kEntries) {
+      if (hit && o < kEntries) {
         L.ent[wave * kEntries + o] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
-        L.etag[wave * kEntries + o] = base | (hm << 24) | ((uint32_t)c << 28);
+        L.etag[wave * kEntries + o] = chunk_pos<NCH>((uint32_t)c, wave, lane) | ((uint32_t)c << 28);
       }
       nent += (uint32_t)__popcll((unsigned long long)m);
     }
   };
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    if (c >= S) prep(c);
-    scan_chunk(c);
-  }
+  for (int c = 0; c < NCH; ++c) scan_chunk(c, mc[c]);
   LLMHIP_MARK(5);
 
   // 5. Settle this wave's entries: each lane takes an entry and handles its
@@ -611,7 +655,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
         tag = L.etag[wave * kEntries + k];
       }
       const uint32_t base = tag & 0x00ffffffu, c = tag >> 28;
-      uint32_t rem = (tag >> 24) & 0xfu;
+      uint32_t rem = k < nent ? ((ev.x >= tf ? 1u : 0u) | (ev.y >= tf ? 2u : 0u) | (ev.z >= tf ? 4u : 0u) |
+                                 (ev.w >= tf ? 8u : 0u))
+                              : 0u;
       // The entry's owner is a lane of this wave: fetch its mask words.
       const uint32_t owner = pos_owner<NCH>(base);
       const uint32_t mkown = final ? 0u : (uint32_t)__builtin_amdgcn_ds_bpermute((int)((owner & 63u) << 2), (int)mkbits);
@@ -677,7 +723,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     // Values are final now (fixed in place).
     nent = 0u;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) scan_chunk(c);
+    for (int c = 0; c < NCH; ++c) scan_chunk(c, max4(c));
     settle(true);
     lds_barrier();
     n = L.misc[kCandN];

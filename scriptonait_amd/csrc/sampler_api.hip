@@ -162,7 +162,6 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.out_probs = out_probs;
   a.out_kept = out_kept;
   a.slotmask = static_cast<const uint32_t*>(ctx->zeros.ptr);
-  a.spec_sampled = V <= kMaxFastV ? fast_spec_sampled((uint32_t)V) : 0u;
   a.status = static_cast<uint32_t*>(ctx->status.ptr);
   a.scratch = static_cast<uint32_t*>(ctx->scratch.ptr);
   a.scratch_row_words = row_words;

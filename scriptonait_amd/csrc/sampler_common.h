@@ -59,9 +59,6 @@ struct SampleArgs {
   // by `allowed` (the fast kernel's layout, built by a prep kernel), or all
   // zeros when there is no mask. 1024 words, always valid.
   const uint32_t* slotmask;
-  // Fast path: number of row positions in the threshold sample (the first
-  // chunks of every wave), computed on the host from V.
-  uint32_t spec_sampled;
   // Device word of kStatus* bits, set by a kernel that hit an internal
   // limit (zero after a correct call).
   uint32_t* status;
@@ -92,19 +89,6 @@ constexpr uint32_t kMaxFastV = 32768;    // largest V of the register path
 // each of the 1024 threads holds NCH float4 chunks of the row.
 __host__ __device__ __forceinline__ uint32_t fast_nch(uint32_t V) {
   return V <= 4096 ? 1u : V <= 8192 ? 2u : V <= 16384 ? 4u : 8u;
-}
-
-// Row positions in the fast kernel's threshold sample: chunks 0..S-1 of
-// every wave, wave w owning the 256-float blocks w*NCH .. w*NCH+NCH-1.
-__host__ __device__ __forceinline__ uint32_t fast_spec_sampled(uint32_t V) {
-  const uint32_t nch = fast_nch(V), S = nch >= 4 ? nch / 4 : 1;
-  uint32_t n = 0;
-  for (uint32_t w = 0; w < kWaves; ++w)
-    for (uint32_t c = 0; c < S; ++c) {
-      const uint32_t s0 = (w * nch + c) * 256u;
-      n += s0 >= V ? 0u : (V - s0 < 256u ? V - s0 : 256u);
-    }
-  return n;
 }
 
 __host__ __device__ __forceinline__ uint32_t row_class(const llmhip_params& p, uint32_t V) {
