@@ -369,6 +369,13 @@ __device__ __forceinline__ void draw_tail_lanes(const SampleArgs& a, uint32_t b,
   if (a.out_probs && lane < stop) a.out_probs[(size_t)b * a.V + my_id] = p;
 }
 
+// Half an f32 ulp in the binade of x (x > 0; values below 2^-60 count as
+// 2^-60), as an f64.
+__device__ __forceinline__ double half_ulp_f32_at(double x) {
+  const uint64_t bits = (uint64_t)__double_as_longlong(fmax(x, 0x1p-60));
+  return __longlong_as_double((long long)((((bits >> 52) & 0x7ffull) - 24ull) << 52));
+}
+
 // The same computation for n <= 64 candidates held one per lane, with the
 // folds as plain dependent adds: the terms are broadcast to every lane
 // through LDS (`buf`, 64 floats, 16-byte aligned) once, and each fold step is
@@ -422,67 +429,122 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
     if (keep < 1u) keep = 1u;
   }
 
-  buf[lane] = p;
-  float4 pv[16];
-#pragma unroll
-  for (int q = 0; q < 16; ++q) pv[q] = b4[q];
-
-  // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; top-p keeps up to the
-  // first c_i >= top_p (all when top_p >= 1 or never reached); the total
-  // over the kept prefix is the fold at its last element. The fold runs in
-  // blocks of 8 dependent adds; c never decreases (p_i >= 0), so only the
-  // last value of a block is tested, and the block that holds the stop (or
-  // the end of the kept prefix) is resolved once, after the loop: lane
-  // 8k+j takes c_{8k+j} and one ballot finds the first c_i >= top_p.
-  const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
-  uint32_t stop = keep;
-  float total;
+  // generate.rs:397-419 without the folds, where that is provably exact.
+  // The top-p fold c_i = ((0 + p_0) + ...) + p_i and the walk r_0 = u*total,
+  // r_{i+1} = r_i - p_i are f32 left folds. Each rounding is at most half
+  // an f32 ulp of its result, and the results are bounded from above by the
+  // exact prefix sums P_i (an f64 wave scan; c_i <= P_i (1 + 2^-17) since
+  // |c_i - P_i| <= i 2^-24 P_i), so
+  //   |c_i - P_i| <= B_i = sum_{k=1..i} hulp(P_k (1 + 2^-17)),
+  // and, while r_j >= p_j for j < i (0 <= r_j <= r_0),
+  //   r_i in [u lo(c_s) - P_{i-1} - G_i, u hi(c_s) - P_{i-1} + G_i],
+  //   G_i = sum_{k=0..i} hulp(upper bound of r_k),
+  // with c_s the total at s = stop - 1 in [P_s - B_s, P_s + B_s]. Each
+  // decision (c_i >= top_p, r_i < p_i) is taken from these intervals plus
+  // an f64 rounding margin; the first decision that is true must be
+  // certainly true and every one before it certainly false. Otherwise (a
+  // near tie) the folds are replayed exactly.
+  uint32_t stop = keep, pick = 0;
+  bool cert = true;
   {
-    float c = 0.0f, cb[8];
-    uint32_t k = 0;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        c += term(pv, 8 * kk + j);
-        cb[j] = c;
+    const double pd = lane < keep ? (double)p : 0.0;
+    const double Pi = wave_incl_scan_f64(pd);
+    const double bk = (lane >= 1u && lane < keep) ? half_ulp_f32_at(Pi * (1.0 + 0x1p-17)) : 0.0;
+    const double Bi = wave_incl_scan_f64(bk) + 0x1p-45 * Pi;
+    if (P.top_p < 1.0f) {
+      const double tpd = (double)P.top_p;
+      const uint64_t poss = __ballot(lane < keep && !(Pi + Bi < tpd));
+      const uint64_t sure = __ballot(lane < keep && Pi - Bi >= tpd);
+      if (poss) {
+        const uint32_t i = (uint32_t)__ffsll((unsigned long long)poss) - 1u;
+        if ((sure >> i) & 1ull) stop = i + 1u;
+        else cert = false;
       }
-      k = (uint32_t)kk;
-      if (c >= tp || 8u * (uint32_t)(kk + 1) >= keep) break;
     }
-    const uint32_t k8 = 8u * k;
-    float t = cb[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) t = lane == k8 + (uint32_t)j ? cb[j] : t;
-    const uint64_t hit = __ballot(lane >= k8 && lane < k8 + 8u && lane < keep && t >= tp);
-    if (hit) stop = (uint32_t)__ffsll((unsigned long long)hit);
-    total = readlane_f32(t, stop - 1u);
+    if (cert) {
+      const uint32_t s = stop - 1u;
+      const double Ps = readlane_f64(Pi, s), Bs = readlane_f64(Bi, s), U = (double)u;
+      const double lo0 = U * (Ps - Bs), hi0 = U * (Ps + Bs);
+      const double Pprev = Pi - pd;  // P_{i-1}
+      const double rup = fmax(hi0 - Pprev, 0.0) * (1.0 + 0x1p-17) + 0x1p-17 * hi0;  // >= r_i
+      const double gk = lane < stop ? half_ulp_f32_at(rup) : 0.0;
+      const double Gi = wave_incl_scan_f64(gk) + 0x1p-45 * (hi0 + Pprev);
+      const double pdd = (double)p;
+      const uint64_t poss = __ballot(lane < stop && !(lo0 - Pprev - Gi >= pdd));
+      const uint64_t sure = __ballot(lane < stop && hi0 - Pprev + Gi < pdd);
+      if (!poss) {
+        pick = stop - 1u;
+      } else {
+        const uint32_t i = (uint32_t)__ffsll((unsigned long long)poss) - 1u;
+        if ((sure >> i) & 1ull) pick = i;
+        else cert = false;
+      }
+    }
   }
 
-  // generate.rs:412-419: r_0 = u * total; step i tests r_i < p_i and then
-  // subtracts p_i. r - p < 0 exactly when r < p (f32 denormals are kept), so
-  // the block holding the pick is the first that ends negative; lane 8k+j
-  // takes r_{8k+j} and compares it with its own p.
-  uint32_t pick = stop - 1u;
-  {
-    float r = u * total, rb[8];
-    uint32_t k = 0;
+  if (!cert) {
+    buf[lane] = p;
+    float4 pv[16];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int q = 0; q < 16; ++q) pv[q] = b4[q];
+
+    // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; top-p keeps up to the
+    // first c_i >= top_p (all when top_p >= 1 or never reached); the total
+    // over the kept prefix is the fold at its last element. The fold runs in
+    // blocks of 8 dependent adds; c never decreases (p_i >= 0), so only the
+    // last value of a block is tested, and the block that holds the stop (or
+    // the end of the kept prefix) is resolved once, after the loop: lane
+    // 8k+j takes c_{8k+j} and one ballot finds the first c_i >= top_p.
+    const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
+    stop = keep;
+    float total;
+    {
+      float c = 0.0f, cb[8];
+      uint32_t k = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        rb[j] = r;
-        r -= term(pv, 8 * kk + j);
+      for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          c += term(pv, 8 * kk + j);
+          cb[j] = c;
+        }
+        k = (uint32_t)kk;
+        if (c >= tp || 8u * (uint32_t)(kk + 1) >= keep) break;
       }
-      k = (uint32_t)kk;
-      if (r < 0.0f || 8u * (uint32_t)(kk + 1) >= stop) break;
-    }
-    const uint32_t k8 = 8u * k;
-    float t = rb[0];
+      const uint32_t k8 = 8u * k;
+      float t = cb[0];
 #pragma unroll
-    for (int j = 1; j < 8; ++j) t = lane == k8 + (uint32_t)j ? rb[j] : t;
-    const uint64_t hit = __ballot(lane >= k8 && lane < k8 + 8u && lane < stop && t < p);
-    if (hit) pick = (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+      for (int j = 1; j < 8; ++j) t = lane == k8 + (uint32_t)j ? cb[j] : t;
+      const uint64_t hit = __ballot(lane >= k8 && lane < k8 + 8u && lane < keep && t >= tp);
+      if (hit) stop = (uint32_t)__ffsll((unsigned long long)hit);
+      total = readlane_f32(t, stop - 1u);
+    }
+
+    // generate.rs:412-419: r_0 = u * total; step i tests r_i < p_i and then
+    // subtracts p_i. r - p < 0 exactly when r < p (f32 denormals are kept), so
+    // the block holding the pick is the first that ends negative; lane 8k+j
+    // takes r_{8k+j} and compares it with its own p.
+    pick = stop - 1u;
+    {
+      float r = u * total, rb[8];
+      uint32_t k = 0;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          rb[j] = r;
+          r -= term(pv, 8 * kk + j);
+        }
+        k = (uint32_t)kk;
+        if (r < 0.0f || 8u * (uint32_t)(kk + 1) >= stop) break;
+      }
+      const uint32_t k8 = 8u * k;
+      float t = rb[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) t = lane == k8 + (uint32_t)j ? rb[j] : t;
+      const uint64_t hit = __ballot(lane >= k8 && lane < k8 + 8u && lane < stop && t < p);
+      if (hit) pick = (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+    }
   }
   const uint32_t id = readlane_u32(my_id, pick);
   if (lane == 0) {

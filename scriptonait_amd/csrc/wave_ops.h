@@ -26,6 +26,25 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   return x;
 }
 
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp0_f64(double x) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = dpp0<CTRL, ROW_MASK>((uint32_t)u), hi = dpp0<CTRL, ROW_MASK>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// The same prefix sum in f64 (lanes read +0.0 where the pattern has no
+// source).
+__device__ __forceinline__ double wave_incl_scan_f64(double x) {
+  x += dpp0_f64<0x111>(x);
+  x += dpp0_f64<0x112>(x);
+  x += dpp0_f64<0x114>(x);
+  x += dpp0_f64<0x118>(x);
+  x += dpp0_f64<0x142, 0xa>(x);
+  x += dpp0_f64<0x143, 0xc>(x);
+  return x;
+}
+
 __device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
 #pragma unroll
   for (uint32_t off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
@@ -52,6 +71,9 @@ __device__ __forceinline__ uint32_t readlane_u32(uint32_t x, uint32_t l) {
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t x, uint32_t l) {
   const uint32_t lo = readlane_u32((uint32_t)x, l), hi = readlane_u32((uint32_t)(x >> 32), l);
   return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ double readlane_f64(double x, uint32_t l) {
+  return __longlong_as_double((long long)readlane_u64((uint64_t)__double_as_longlong(x), l));
 }
 
 // Number of set bits of the wave mask m in lanes below this one.

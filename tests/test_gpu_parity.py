@@ -128,3 +128,54 @@ def test_long_history_with_repeats(sampler):
 
     o = oracle.sample_batch(w.logits, w.params, w.rng_seeds, hist, offs, V=w.V, want_probs=True)
     compare(g, o, "long history")
+
+
+_GOLDEN = 0x9E3779B97F4A7C15
+_M1, _M2 = 0xBF58476D1CE4E5B9, 0x94D049BB133111EB
+_MASK = (1 << 64) - 1
+
+
+def _seed_for_draw(m24: int) -> int:
+    """A SplitMix64 seed whose first f32 draw (rng.rs:24-34: the top 24 bits
+    of the first output, times 2^-24) is exactly m24 * 2^-24. The output mix
+    is a bijection; this runs it backwards."""
+    def unxorshift(z, s):
+        x = z
+        for _ in range(64 // s + 1):
+            x = z ^ (x >> s)
+        return x & _MASK
+    z = (m24 << 40) & _MASK
+    z = unxorshift(z, 31)
+    z = (z * pow(_M2, -1, 1 << 64)) & _MASK
+    z = unxorshift(z, 27)
+    z = (z * pow(_M1, -1, 1 << 64)) & _MASK
+    z = unxorshift(z, 30)
+    return (z - _GOLDEN) & _MASK
+
+
+@pytest.mark.parametrize("V", [4096, 32000])
+def test_exact_ties_in_the_top_p_and_draw_folds(sampler, V):
+    """64 equal top values give p_i = 1/64 and exact cumulative sums: top-p
+    cut-offs that land exactly on a cumulative value and draws that land
+    exactly on a walk boundary, where only an exact replay of the f32 folds
+    decides (generate.rs:397-419)."""
+    from oracle import oracle
+    from scriptonait_amd.workloads import splitmix64_outputs
+
+    assert splitmix64_outputs(_seed_for_draw(0x400000), 1)[0] >> np.uint64(40) == 0x400000
+    rs = np.random.default_rng(5)
+    B = 96
+    logits = (rs.standard_normal((B, V)) - 20.0).astype(np.float32)
+    for b in range(B):
+        logits[b, rs.choice(V, 64, replace=False)] = 5.0
+    prm = np.zeros(B, dtype=PARAMS_DTYPE)
+    seeds = np.zeros(B, dtype=np.uint64)
+    for b in range(B):
+        top_p = [0.5, 0.25, 1.0, 0.75 + 2.0 ** -20][b % 4]
+        prm[b] = (1.0, 64, top_p, [0.0, 0.5][b % 2], 1.0)
+        seeds[b] = _seed_for_draw((b % 32) << 19)  # u = (b % 32) / 32: exact walk boundaries
+    g = sampler.sample_host(logits, prm, seeds, want_probs=True)
+    o = oracle.sample_batch(logits, prm, seeds, want_probs=True)
+    assert np.array_equal(g.ids, o.ids), np.nonzero(g.ids != o.ids)[0]
+    assert np.array_equal(g.kept, o.kept)
+    assert np.array_equal(g.rng_state, o.rng_state)
