@@ -432,13 +432,13 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
   // generate.rs:397-419 without the folds, where that is provably exact.
   // The top-p fold c_i = ((0 + p_0) + ...) + p_i and the walk r_0 = u*total,
   // r_{i+1} = r_i - p_i are f32 left folds. Each rounding is at most half
-  // an f32 ulp of its result, and the results are bounded from above by the
-  // exact prefix sums P_i (an f64 wave scan; c_i <= P_i (1 + 2^-17) since
-  // |c_i - P_i| <= i 2^-24 P_i), so
-  //   |c_i - P_i| <= B_i = sum_{k=1..i} hulp(P_k (1 + 2^-17)),
-  // and, while r_j >= p_j for j < i (0 <= r_j <= r_0),
+  // an f32 ulp (hulp) of its result. The c_k never decrease and are bounded
+  // by the exact prefix sums P_i (an f64 wave scan): c_k <= c_i <=
+  // P_i (1 + 2^-17) for k <= i, since |c_i - P_i| <= i 2^-24 P_i. So
+  //   |c_i - P_i| <= B_i = i hulp(P_i (1 + 2^-17)),
+  // and, while r_j >= p_j for j < i (then 0 <= r_j <= r_0),
   //   r_i in [u lo(c_s) - P_{i-1} - G_i, u hi(c_s) - P_{i-1} + G_i],
-  //   G_i = sum_{k=0..i} hulp(upper bound of r_k),
+  //   G_i = (i + 1) hulp(u hi(c_s) (1 + 2^-16)),
   // with c_s the total at s = stop - 1 in [P_s - B_s, P_s + B_s]. Each
   // decision (c_i >= top_p, r_i < p_i) is taken from these intervals plus
   // an f64 rounding margin; the first decision that is true must be
@@ -449,8 +449,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
   {
     const double pd = lane < keep ? (double)p : 0.0;
     const double Pi = wave_incl_scan_f64(pd);
-    const double bk = (lane >= 1u && lane < keep) ? half_ulp_f32_at(Pi * (1.0 + 0x1p-17)) : 0.0;
-    const double Bi = wave_incl_scan_f64(bk) + 0x1p-45 * Pi;
+    const double Bi = (double)lane * half_ulp_f32_at(Pi * (1.0 + 0x1p-17)) + 0x1p-45 * Pi;
     if (P.top_p < 1.0f) {
       const double tpd = (double)P.top_p;
       const uint64_t poss = __ballot(lane < keep && !(Pi + Bi < tpd));
@@ -466,9 +465,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
       const double Ps = readlane_f64(Pi, s), Bs = readlane_f64(Bi, s), U = (double)u;
       const double lo0 = U * (Ps - Bs), hi0 = U * (Ps + Bs);
       const double Pprev = Pi - pd;  // P_{i-1}
-      const double rup = fmax(hi0 - Pprev, 0.0) * (1.0 + 0x1p-17) + 0x1p-17 * hi0;  // >= r_i
-      const double gk = lane < stop ? half_ulp_f32_at(rup) : 0.0;
-      const double Gi = wave_incl_scan_f64(gk) + 0x1p-45 * (hi0 + Pprev);
+      const double Gi = (double)(lane + 1u) * half_ulp_f32_at(hi0 * (1.0 + 0x1p-16)) + 0x1p-45 * (hi0 + Pprev);
       const double pdd = (double)p;
       const uint64_t poss = __ballot(lane < stop && !(lo0 - Pprev - Gi >= pdd));
       const uint64_t sure = __ballot(lane < stop && hi0 - Pprev + Gi < pdd);
