@@ -1,7 +1,7 @@
 """GPU parity: the HIP sampler against the CPU oracle on the same bytes.
 
 Configs 1-3 run at their full BASELINE sizes; configs 4-5 (the full-vocab
-path) at reduced batch here and at full size in test_gpu_full_sizes.py.
+path) at reduced batch.
 """
 import numpy as np
 import pytest
