@@ -120,255 +120,6 @@ __device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const
   }
 }
 
-// Same computation for n <= 64 candidates held one per lane (lane i holds
-// candidate i's key and id; lanes >= n are ignored), with the RNG state
-// already in a register. Each fold is a chain of dependent VGPR adds over
-// all 64 values, fetched from LDS (`buf`, 128 floats) into registers up
-// front; padding lanes contribute +0.0, which leaves an f32 sum of
-// non-negative terms unchanged. Running values are parked in LDS so that
-// lane i can test its own prefix, and a ballot finds the first lane that
-// decides (the reference's early `break`).
-__device__ __forceinline__ void draw_tail_small(const SampleArgs& a, uint32_t b, const llmhip_params& P,
-                                                uint32_t n, uint32_t my_key, uint32_t my_id,
-                                                uint64_t st, float* buf, const uint64_t* tab) {
-  const uint32_t lane = lane_id();
-  const bool act = lane < n;
-  const uint32_t k0 = readlane_u32(my_key, 0);
-  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
-  const float e = act ? glibc_expf_tab(key2f(my_key) - mx, tab) : 0.0f;
-  float* cbuf = buf + 64;
-  const float4* b4 = reinterpret_cast<const float4*>(buf);
-
-  // generate.rs:374
-  buf[lane] = e;
-  float sum = 0.0f;
-  {
-    float4 v[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) v[q] = b4[q];
-    bool go = true;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      if (go) {
-        sum += v[q].x;
-        sum += v[q].y;
-        sum += v[q].z;
-        sum += v[q].w;
-        if ((q & 1) && 4u * (q + 1) >= n) go = false;
-      }
-    }
-  }
-  // generate.rs:375-377
-  if (!(sum > 0.0f) || !isfinite(sum)) {
-    if (lane == 0) {
-      a.out_ids[b] = n > 0 ? my_id : 0u;
-      if (a.out_kept) a.out_kept[b] = 0u;
-    }
-    return;
-  }
-  const float p = act ? e / sum : 0.0f;  // generate.rs:378-380
-
-  // generate.rs:384-395
-  uint32_t keep = n;
-  if (P.min_p > 0.0f) {
-    const float thr = P.min_p * readlane_f32(p, 0);
-    const uint64_t fail = __ballot(act && !(p >= thr));
-    if (fail) keep = (uint32_t)__ffsll((unsigned long long)fail) - 1u;
-    if (keep < 1u) keep = 1u;
-  }
-
-  // generate.rs:397-411: c_i = fold of p_0..p_i; lane i reads its c_i. The
-  // total over a kept prefix is that fold at its last element.
-  buf[lane] = p;
-  float4 pv[16];
-#pragma unroll
-  for (int q = 0; q < 16; ++q) pv[q] = b4[q];
-  {
-    // Stops after the block of 8 where the fold reaches top_p (every lane
-    // holds the same running value, so the exit is uniform).
-    const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
-    float c = 0.0f;
-    bool go = true;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      if (go) {
-        float4 o;
-        c += pv[q].x;
-        o.x = c;
-        c += pv[q].y;
-        o.y = c;
-        c += pv[q].z;
-        o.z = c;
-        c += pv[q].w;
-        o.w = c;
-        if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
-        // c is the same in every lane: read it as a scalar.
-        if ((q & 1) && (4u * (q + 1) >= keep || __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(c))) >= tp)) go = false;
-      }
-    }
-  }
-  const float my_c = lane < keep ? cbuf[lane] : 0.0f;
-  uint32_t stop = keep;
-  if (P.top_p < 1.0f) {
-    const uint64_t hit = __ballot(lane < keep && my_c >= P.top_p);
-    if (hit) stop = (uint32_t)__ffsll((unsigned long long)hit);
-  }
-  const float total = readlane_f32(my_c, stop - 1u);
-
-  // generate.rs:412-419: r_i = r before subtracting p_i; lane i tests r_i < p_i.
-  const float ur = next_f32(st);
-  {
-    // r - p < 0 exactly when r < p, so r turns negative at the pick: stop
-    // after that block of 8.
-    float r = ur * total;
-    bool go = true;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      if (go) {
-        float4 o;
-        o.x = r;
-        r -= pv[q].x;
-        o.y = r;
-        r -= pv[q].y;
-        o.z = r;
-        r -= pv[q].z;
-        o.w = r;
-        r -= pv[q].w;
-        if (lane == 0) reinterpret_cast<float4*>(cbuf)[q] = o;
-        if ((q & 1) && (4u * (q + 1) >= stop || __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(r))) < 0.0f)) go = false;
-      }
-    }
-  }
-  const float my_r = lane < stop ? cbuf[lane] : 0.0f;
-  const uint64_t hit = __ballot(lane < stop && my_r < p);
-  const uint32_t pick = hit ? (uint32_t)__ffsll((unsigned long long)hit) - 1u : stop - 1u;
-  const uint32_t id = readlane_u32(my_id, pick);
-  if (lane == 0) {
-    a.out_ids[b] = id;
-    a.rng_state[b] = st;
-    if (a.out_kept) a.out_kept[b] = stop;
-  }
-  if (a.out_probs && lane < stop) a.out_probs[(size_t)b * a.V + my_id] = p;
-}
-
-// Lane i's value of x from lane i-1 (lane 0 gets `first`): DPP wave_shr:1.
-__device__ __forceinline__ float from_prev_lane(float x, float first) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(x), 0x138, 0xf, 0xf, false));
-}
-
-// Eight steps of a running left fold spread over the lanes: each step sets
-// lane i to fl(acc[i-1] + v[i]) (fold_add8) or fl(acc[i-1] - v[i])
-// (fold_sub8), one v_add/v_sub_f32 with a DPP wave_shr:1 source. Lane 0 has
-// no lane before it: the write is disabled there (no bound_ctrl), so it
-// keeps its value. A DPP read of a VGPR written by the previous VALU
-// instruction needs two wait states (s_nop 1).
-#define LLMHIP_FOLD_STEP(op) "s_nop 1\n\t" op " %0, %0, %1 wave_shr:1 row_mask:0xf bank_mask:0xf\n\t"
-__device__ __forceinline__ float fold_add8(float acc, float v) {
-  asm volatile(LLMHIP_FOLD_STEP("v_add_f32_dpp") LLMHIP_FOLD_STEP("v_add_f32_dpp")
-               LLMHIP_FOLD_STEP("v_add_f32_dpp") LLMHIP_FOLD_STEP("v_add_f32_dpp")
-               LLMHIP_FOLD_STEP("v_add_f32_dpp") LLMHIP_FOLD_STEP("v_add_f32_dpp")
-               LLMHIP_FOLD_STEP("v_add_f32_dpp") LLMHIP_FOLD_STEP("v_add_f32_dpp")
-               : "+v"(acc)
-               : "v"(v));
-  return acc;
-}
-__device__ __forceinline__ float fold_sub8(float acc, float v) {
-  asm volatile(LLMHIP_FOLD_STEP("v_sub_f32_dpp") LLMHIP_FOLD_STEP("v_sub_f32_dpp")
-               LLMHIP_FOLD_STEP("v_sub_f32_dpp") LLMHIP_FOLD_STEP("v_sub_f32_dpp")
-               LLMHIP_FOLD_STEP("v_sub_f32_dpp") LLMHIP_FOLD_STEP("v_sub_f32_dpp")
-               LLMHIP_FOLD_STEP("v_sub_f32_dpp") LLMHIP_FOLD_STEP("v_sub_f32_dpp")
-               : "+v"(acc)
-               : "v"(v));
-  return acc;
-}
-#undef LLMHIP_FOLD_STEP
-
-// The same computation for n <= 64 candidates held one per lane (lane i
-// holds candidate i's key and id; lanes >= n are ignored). Each sequential
-// fold of the reference runs as a chain of DPP wave-shift adds: step t sets
-// lane i to (lane i-1's running value) op (lane i's term), so after t steps
-// lanes 0..t hold exactly the reference's running values, rounding for
-// rounding, and no value leaves the registers. u is the uniform draw and
-// st_next the RNG state after it (both computed ahead of the tail).
-__device__ __forceinline__ void draw_tail_lanes(const SampleArgs& a, uint32_t b, const llmhip_params& P,
-                                                uint32_t n, uint32_t my_key, uint32_t my_id, float u,
-                                                uint64_t st_next, const uint64_t* tab) {
-  const uint32_t lane = lane_id();
-  const bool act = lane < n;
-  const uint32_t k0 = readlane_u32(my_key, 0);
-  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
-  const float e = act ? glibc_expf_tab(key2f(my_key) - mx, tab) : 0.0f;
-
-  // generate.rs:374: sum = ((0 + e_0) + e_1) + ...; lane n-1 ends with it.
-  // Lane 0 holds 0 + e_0 = e_0 throughout; steps past n-1 change nothing
-  // in lanes 0..n-1.
-  float s = e;
-  for (uint32_t t = 1; t < n; t += 8) s = fold_add8(s, e);
-  const float sum = readlane_f32(s, n - 1u);
-  // generate.rs:375-377: degenerate exit, no draw.
-  if (!(sum > 0.0f) || !isfinite(sum)) {
-    if (lane == 0) {
-      a.out_ids[b] = n > 0 ? my_id : 0u;
-      if (a.out_kept) a.out_kept[b] = 0u;
-    }
-    return;
-  }
-  const float p = act ? e / sum : 0.0f;  // generate.rs:378-380
-
-  // generate.rs:384-395: longest prefix with p >= min_p * p_0, at least 1.
-  uint32_t keep = n;
-  if (P.min_p > 0.0f) {
-    const float thr = P.min_p * readlane_f32(p, 0);
-    const uint64_t fail = __ballot(act && !(p >= thr));
-    if (fail) keep = (uint32_t)__ffsll((unsigned long long)fail) - 1u;
-    if (keep < 1u) keep = 1u;
-  }
-
-  // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; top-p keeps up to
-  // the first c_i >= top_p. The total over the kept prefix is that fold at
-  // its last element. Checked every 8 steps (lanes 0..t are exact).
-  const bool use_tp = P.top_p < 1.0f;
-  float c = p;
-  uint32_t stop = keep;
-  for (uint32_t t = 0;;) {
-    if (use_tp) {
-      const uint64_t hit = __ballot(lane <= t && lane < keep && c >= P.top_p);
-      if (hit) {
-        stop = (uint32_t)__ffsll((unsigned long long)hit);
-        break;
-      }
-    }
-    if (t + 1u >= keep) break;
-    c = fold_add8(c, p);
-    t += 8u;
-  }
-  const float total = readlane_f32(c, stop - 1u);
-
-  // generate.rs:412-419: r_0 = u * total; lane i tests r_i < p_i with
-  // r_i = r_{i-1} - p_{i-1}.
-  const float r0 = u * total;
-  const float pm1 = from_prev_lane(p, 0.0f);  // lane i: p_{i-1}
-  float r = r0;  // lane 0 keeps r_0
-  uint32_t pick = stop - 1u;
-  for (uint32_t t = 0;;) {
-    const uint64_t hit = __ballot(lane <= t && lane < stop && r < p);
-    if (hit) {
-      pick = (uint32_t)__ffsll((unsigned long long)hit) - 1u;
-      break;
-    }
-    if (t + 1u >= stop) break;
-    r = fold_sub8(r, pm1);
-    t += 8u;
-  }
-  const uint32_t id = readlane_u32(my_id, pick);
-  if (lane == 0) {
-    a.out_ids[b] = id;
-    a.rng_state[b] = st_next;
-    if (a.out_kept) a.out_kept[b] = stop;
-  }
-  if (a.out_probs && lane < stop) a.out_probs[(size_t)b * a.V + my_id] = p;
-}
-
 // Half an f32 ulp in the binade of x (x > 0; values below 2^-60 count as
 // 2^-60), as an f64.
 __device__ __forceinline__ double half_ulp_f32_at(double x) {
@@ -376,14 +127,12 @@ __device__ __forceinline__ double half_ulp_f32_at(double x) {
   return __longlong_as_double((long long)((((bits >> 52) & 0x7ffull) - 24ull) << 52));
 }
 
-// The same computation for n <= 64 candidates held one per lane, with the
-// folds as plain dependent adds: the terms are broadcast to every lane
-// through LDS (`buf`, 64 floats, 16-byte aligned) once, and each fold step is
-// then one v_add on registers. The folds run in blocks of 8 whose running
-// values stay in registers; a block is checked once (a running sum is
-// monotone: the terms are non-negative) and the deciding step inside it is
-// found by compares on the kept values. Padding terms are +0.0, which leaves
-// a sum of non-negative f32 terms unchanged.
+// The same computation for n <= 64 candidates held one per lane. The
+// softmax sum runs as 64 dependent adds over terms broadcast through LDS
+// (`buf`, 64 floats, 16-byte aligned); padding terms are +0.0, which leaves a
+// sum of non-negative f32 terms unchanged. Top-p and the draw are decided from
+// f64 prefix sums with error bounds, and the folds are replayed exactly only
+// on a near tie (below).
 __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b, const llmhip_params& P,
                                                 uint32_t n, uint32_t my_key, uint32_t my_id, float u,
                                                 uint64_t st_next, const uint64_t* tab, float* buf) {
@@ -393,22 +142,31 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
   const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
   const float e = act ? glibc_expf_tab(key2f(my_key) - mx, tab) : 0.0f;
   const float4* b4 = reinterpret_cast<const float4*>(buf);
-  auto term = [](const float4 (&q)[16], int i) __attribute__((always_inline)) {
-    const float4& f = q[i >> 2];
-    return (i & 3) == 0 ? f.x : (i & 3) == 1 ? f.y : (i & 3) == 2 ? f.z : f.w;
+  auto term4 = [](const float4& f, int i) __attribute__((always_inline)) {
+    return i == 0 ? f.x : i == 1 ? f.y : i == 2 ? f.z : f.w;
   };
 
   // generate.rs:374: sum = ((0 + e_0) + e_1) + ... over the n terms, as 64
   // dependent adds: the terms past n are +0, which leave a sum >= e_0 = 1
-  // (or a NaN one) unchanged.
+  // (or a NaN one) unchanged. The terms come in four batches of 16, the
+  // next batch loading while the current one is added.
   buf[lane] = e;
   float sum = 0.0f;
   {
-    float4 w[16];
+    float4 wc[4], wn[4];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) w[q] = b4[q];
+    for (int q = 0; q < 4; ++q) wc[q] = b4[q];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) sum += term(w, i);
+    for (int h = 0; h < 4; ++h) {
+      if (h < 3) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wn[q] = b4[4 * (h + 1) + q];
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sum += term4(wc[i >> 2], i & 3);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wc[q] = wn[q];
+    }
   }
   // generate.rs:375-377: degenerate exit, no draw.
   if (!(sum > 0.0f) || !isfinite(sum)) {
@@ -481,9 +239,12 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
 
   if (!cert) {
     buf[lane] = p;
-    float4 pv[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) pv[q] = b4[q];
+    // Terms 8k .. 8k+7, read from LDS per block (broadcast).
+    auto block = [&](int kk, float (&t8)[8]) __attribute__((always_inline)) {
+      const float4 lo = b4[2 * kk], hi = b4[2 * kk + 1];
+      t8[0] = lo.x; t8[1] = lo.y; t8[2] = lo.z; t8[3] = lo.w;
+      t8[4] = hi.x; t8[5] = hi.y; t8[6] = hi.z; t8[7] = hi.w;
+    };
 
     // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; top-p keeps up to the
     // first c_i >= top_p (all when top_p >= 1 or never reached); the total
@@ -500,9 +261,11 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
       uint32_t k = 0;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
+        float t8[8];
+        block(kk, t8);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          c += term(pv, 8 * kk + j);
+          c += t8[j];
           cb[j] = c;
         }
         k = (uint32_t)kk;
@@ -527,10 +290,12 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
       uint32_t k = 0;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
+        float t8[8];
+        block(kk, t8);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           rb[j] = r;
-          r -= term(pv, 8 * kk + j);
+          r -= t8[j];
         }
         k = (uint32_t)kk;
         if (r < 0.0f || 8u * (uint32_t)(kk + 1) >= stop) break;
@@ -542,102 +307,6 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
       const uint64_t hit = __ballot(lane >= k8 && lane < k8 + 8u && lane < stop && t < p);
       if (hit) pick = (uint32_t)__ffsll((unsigned long long)hit) - 1u;
     }
-  }
-  const uint32_t id = readlane_u32(my_id, pick);
-  if (lane == 0) {
-    a.out_ids[b] = id;
-    a.rng_state[b] = st_next;
-    if (a.out_kept) a.out_kept[b] = stop;
-  }
-  if (a.out_probs && lane < stop) a.out_probs[(size_t)b * a.V + my_id] = p;
-}
-
-// The same computation for n <= 64 candidates whose softmax numerators
-// e_i = exp(w_i - max) are already in se[0..63] in sorted order (se[i] = 0
-// for i >= n), lane i holding candidate i's id. The sum runs as plain
-// dependent adds over the terms read once into every lane; the top-p and
-// draw folds run as DPP chains over the per-lane probabilities (as in
-// draw_tail_lanes).
-__device__ __forceinline__ void draw_tail_e(const SampleArgs& a, uint32_t b, const llmhip_params& P, uint32_t n,
-                                            const float* se, uint32_t my_id, float u, uint64_t st_next) {
-  const uint32_t lane = lane_id();
-  const bool act = lane < n;
-  const float e = se[lane];
-  const float4* b4 = reinterpret_cast<const float4*>(se);
-
-  // generate.rs:374: sum = ((0 + e_0) + e_1) + ... over the n terms (the
-  // zero padding of a block leaves the sum unchanged).
-  float sum = 0.0f;
-  {
-    float4 w[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) w[q] = b4[q];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (8u * k >= n) break;
-#pragma unroll
-      for (int q = 2 * k; q < 2 * k + 2; ++q) {
-        sum += w[q].x;
-        sum += w[q].y;
-        sum += w[q].z;
-        sum += w[q].w;
-      }
-    }
-  }
-  // generate.rs:375-377: degenerate exit, no draw.
-  if (!(sum > 0.0f) || !isfinite(sum)) {
-    if (lane == 0) {
-      a.out_ids[b] = n > 0 ? my_id : 0u;
-      if (a.out_kept) a.out_kept[b] = 0u;
-    }
-    return;
-  }
-  const float p = act ? e / sum : 0.0f;  // generate.rs:378-380
-
-  // generate.rs:384-395: longest prefix with p >= min_p * p_0, at least 1.
-  uint32_t keep = n;
-  if (P.min_p > 0.0f) {
-    const float thr = P.min_p * readlane_f32(p, 0);
-    const uint64_t fail = __ballot(act && !(p >= thr));
-    if (fail) keep = (uint32_t)__ffsll((unsigned long long)fail) - 1u;
-    if (keep < 1u) keep = 1u;
-  }
-
-  // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; top-p keeps up to
-  // the first c_i >= top_p. The total over the kept prefix is that fold at
-  // its last element. Checked every 8 steps (lanes 0..t are exact).
-  const bool use_tp = P.top_p < 1.0f;
-  float c = p;
-  uint32_t stop = keep;
-  for (uint32_t t = 0;;) {
-    if (use_tp) {
-      const uint64_t hit = __ballot(lane <= t && lane < keep && c >= P.top_p);
-      if (hit) {
-        stop = (uint32_t)__ffsll((unsigned long long)hit);
-        break;
-      }
-    }
-    if (t + 1u >= keep) break;
-    c = fold_add8(c, p);
-    t += 8u;
-  }
-  const float total = readlane_f32(c, stop - 1u);
-
-  // generate.rs:412-419: r_0 = u * total; lane i tests r_i < p_i with
-  // r_i = r_{i-1} - p_{i-1}.
-  const float r0 = u * total;
-  const float pm1 = from_prev_lane(p, 0.0f);  // lane i: p_{i-1}
-  float r = r0;  // lane 0 keeps r_0
-  uint32_t pick = stop - 1u;
-  for (uint32_t t = 0;;) {
-    const uint64_t hit = __ballot(lane <= t && lane < stop && r < p);
-    if (hit) {
-      pick = (uint32_t)__ffsll((unsigned long long)hit) - 1u;
-      break;
-    }
-    if (t + 1u >= stop) break;
-    r = fold_sub8(r, pm1);
-    t += 8u;
   }
   const uint32_t id = readlane_u32(my_id, pick);
   if (lane == 0) {
