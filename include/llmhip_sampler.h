@@ -122,8 +122,9 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
                        uint32_t* out_kept);
 
 /*
- * The same computation on DEVICE buffers (all pointers are device
- * pointers, same meaning as above), stream-ordered on `stream` (a
+ * The same computation on DEVICE buffers (every pointer except `params`,
+ * which stays on the host and is copied, is a device pointer; same meaning
+ * as above), stream-ordered on `stream` (a
  * hipStream_t; null = the default stream). Returns after enqueueing; the
  * results are ready when the stream reaches that point. For decode loops
  * whose logits, history and RNG state already live in HBM: nothing crosses
@@ -136,6 +137,35 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
                          const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
                          uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
                          uint32_t* out_kept, void* stream);
+
+/*
+ * One decode step for B generations whose state lives in HBM
+ * (Generator::step with recent_tokens, crates/llm-core/src/generate.rs:
+ * 157-165 and 178-182). For every row b with done[b] == 0 it samples from
+ * the row's logits exactly as llmhip_sample_device does, with `recent` =
+ * the last min(ring_len[b], window) tokens of the row's history, then
+ *   - at eos_id: sets done[b] = 1 (Generator::step returns None), and
+ *   - otherwise: appends the token, ring[b*ring_cap + ring_len[b] %
+ *     ring_cap] = id, ring_len[b] += 1 (Generator::advance).
+ * Rows with done[b] != 0 are skipped: out_ids[b] = eos_id, no draw. The
+ * model's forward pass for the appended token is the caller's. Nothing
+ * crosses PCIe; stream-ordered on `stream` like llmhip_sample_device.
+ *
+ *   ring      device [B][ring_cap] u32: row b's token history (prompt and
+ *             generated tokens) as a ring; the caller fills it with the
+ *             prompt and sets ring_len
+ *   ring_len  device [B] u32 in/out: tokens row b has seen so far
+ *   done      device nullable [B] u32 in/out
+ *   window    repetition_window (SamplingConfig, generate.rs:25-80), at
+ *             most ring_cap
+ * params is a host pointer, as in llmhip_sample_device; logits, allowed,
+ * rng_state and out_ids are device pointers.
+ */
+int llmhip_decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                       const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
+                       uint32_t* ring_len, uint32_t* done, size_t window, const uint8_t* allowed,
+                       size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
+                       void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,12 +14,13 @@
 namespace llmhip {
 
 // key_at(i) / id_at(i): i-th candidate (i < n) in sorted order; st is row
-// b's RNG state and tab the exp table (kExp2fTab or an LDS copy of it).
+// b's RNG state, tab the exp table (kExp2fTab or an LDS copy of it) and
+// len_b the row's ring length (decode-step mode).
 // Must be called by all 64 lanes of exactly one wave. Writes out_ids,
 // rng_state, out_kept and (if requested) out_probs for row b.
 template <class KeyAt, class IdAt>
-__device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const llmhip_params& P, uint32_t n,
-                          KeyAt key_at, IdAt id_at, uint64_t st, const uint64_t* tab) {
+__device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, uint32_t len_b, const llmhip_params& P,
+                          uint32_t n, KeyAt key_at, IdAt id_at, uint64_t st, const uint64_t* tab) {
   const uint32_t lane = lane_id();
   const uint32_t k0 = key_at(0);
   // fold(NEG_INFINITY, f32::max) over sorted candidates: the first one
@@ -38,7 +39,7 @@ __device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const
   // generate.rs:375-377: degenerate exit, no draw.
   if (!(sum > 0.0f) || !isfinite(sum)) {
     if (lane == 0) {
-      a.out_ids[b] = n > 0 ? id_at(0) : 0u;
+      store_result(a, b, n > 0 ? id_at(0) : 0u, len_b);
       if (a.out_kept) a.out_kept[b] = 0u;
     }
     return;
@@ -110,7 +111,7 @@ __device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, const
     }
   }
   if (lane == 0) {
-    a.out_ids[b] = id_at(pick);
+    store_result(a, b, id_at(pick), len_b);
     a.rng_state[b] = st;
     if (a.out_kept) a.out_kept[b] = keep;
   }
@@ -133,8 +134,9 @@ __device__ __forceinline__ double half_ulp_f32_at(double x) {
 // sum of non-negative f32 terms unchanged. Top-p and the draw are decided from
 // f64 prefix sums with error bounds, and the folds are replayed exactly only
 // on a near tie (below).
-__device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b, const llmhip_params& P,
-                                                uint32_t n, uint32_t my_key, uint32_t my_id, float u,
+__device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b, uint32_t len_b,
+                                                const llmhip_params& P, uint32_t n, uint32_t my_key,
+                                                uint32_t my_id, float u,
                                                 uint64_t st_next, const uint64_t* tab, float* buf) {
   const uint32_t lane = lane_id();
   const bool act = lane < n;
@@ -171,7 +173,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
   // generate.rs:375-377: degenerate exit, no draw.
   if (!(sum > 0.0f) || !isfinite(sum)) {
     if (lane == 0) {
-      a.out_ids[b] = n > 0 ? my_id : 0u;
+      store_result(a, b, n > 0 ? my_id : 0u, len_b);
       if (a.out_kept) a.out_kept[b] = 0u;
     }
     return;
@@ -310,7 +312,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
   }
   const uint32_t id = readlane_u32(my_id, pick);
   if (lane == 0) {
-    a.out_ids[b] = id;
+    store_result(a, b, id, len_b);
     a.rng_state[b] = st_next;
     if (a.out_kept) a.out_kept[b] = stop;
   }

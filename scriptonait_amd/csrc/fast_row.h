@@ -382,7 +382,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // row's loads, and the LDS barrier below would wait for them).
   asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.params), "s"(a.params_stride), "s"(a.hist),
                "s"(a.hist_offsets), "s"(a.slotmask), "s"(a.status), "s"(a.rng_state), "s"(a.out_ids),
-               "s"(a.out_probs), "s"(a.out_kept), "s"(a.row_class_mask));
+               "s"(a.out_probs), "s"(a.out_kept), "s"(a.row_class_mask), "s"(a.ring), "s"(a.ring_len),
+               "s"(a.done), "s"(a.ring_cap), "s"(a.window));
   asm volatile("" ::"s"(a.shared.temperature), "s"(a.shared.top_k), "s"(a.shared.top_p), "s"(a.shared.min_p),
                "s"(a.shared.repetition_penalty), "s"(a.eos_id), "s"(a.allowed), "s"(a.allowed_len), "s"(a.B),
                "s"(a.scratch), "s"(a.scratch_row_words));
@@ -401,8 +402,13 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // which count in order with the row's loads: a scalar load would share its
   // counter with LDS operations, and every LDS wait before it returned
   // (behind the row) would wait for it.
-  const bool has_hist = a.hist_offsets && a.hist;
-  const uint32_t hv = (has_hist ? a.hist_offsets + b : a.slotmask)[lane & 1u];
+  // hv: lanes 0-1 read hist_offsets[b], [b+1] (CSR) or ring_len[b], done[b]
+  // (decode-step mode).
+  const bool ring = a.ring_cap != 0u;
+  const bool has_hist = ring || (a.hist_offsets && a.hist);
+  const uint32_t* hvsrc = ring ? ((lane & 1u) && a.done ? a.done + b : a.ring_len + b)
+                               : (has_hist ? a.hist_offsets + b + (lane & 1u) : a.slotmask);
+  const uint32_t hv = *hvsrc;
   const uint32_t rv = reinterpret_cast<const uint32_t*>(a.rng_state + b)[lane & 1u];
   const uint32_t pw =
       a.params ? reinterpret_cast<const uint32_t*>(a.params + (size_t)b * a.params_stride)[min(lane, 4u)] : 0u;
@@ -442,6 +448,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   __builtin_amdgcn_sched_barrier(0);
 
   const uint32_t h0 = has_hist ? readlane_u32(hv, 0) : 0u, h1 = has_hist ? readlane_u32(hv, 1) : 0u;
+  const uint32_t len_b = h0;  // ring length (decode-step mode)
   const uint64_t rng0 = ((uint64_t)readlane_u32(rv, 1) << 32) | readlane_u32(rv, 0);
   llmhip_params P = a.shared;
   if (a.params) {
@@ -452,16 +459,16 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     P.repetition_penalty = __uint_as_float(readlane_u32(pw, 4));
   }
   const float T = P.temperature, rp = P.repetition_penalty;
-  const uint32_t H = (rp != 1.0f && h1 > h0) ? h1 - h0 : 0u;
+  const HistRow hr = hist_row(a, b, h0, h1);
+  const uint32_t H = rp != 1.0f ? hr.H : 0u;
   const bool use_pen = H > 0 && H < 65536u;
   // History ids: lane t of the workgroup fetches ids t, t+1024, ...; they
   // land right behind the wave's part of the row.
   uint32_t hid[kHistPerThread];
   {
-    const uint32_t* hsrc = use_pen ? a.hist + h0 : a.slotmask;
     const uint32_t hmax = use_pen ? H - 1u : 0u;
 #pragma unroll
-    for (uint32_t u = 0; u < kHistPerThread; ++u) hid[u] = hsrc[min(tid + u * kBlock, hmax)];
+    for (uint32_t u = 0; u < kHistPerThread; ++u) hid[u] = use_pen ? hr.at(min(tid + u * kBlock, hmax)) : a.slotmask[0];
   }
   __builtin_amdgcn_sched_barrier(0);
   // This wave's share of the count table (only when a history may be used).
@@ -487,6 +494,14 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
 
   const uint32_t cls = row_class(P, V);
   if (!(cls & a.row_class_mask)) return true;
+  // Decode-step mode: a finished generation is skipped (no draw).
+  if (ring && a.done && h1 != 0u) {
+    if (tid == 0) {
+      a.out_ids[b] = a.eos_id;
+      if (a.out_kept) a.out_kept[b] = 0u;
+    }
+    return true;
+  }
   if (H >= 65536u) return false;  // a u16 multiplicity could overflow
   const bool greedy = cls == kClassGreedy;
   // A penalty below 1 (or NaN) can raise a value above the raw one, so the
@@ -513,7 +528,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
 #pragma unroll
       for (uint32_t u = 0; u < kHistPerThread; ++u)
         if (tid + u * kBlock < H) add_hist(hid[u]);
-      for (uint32_t j = tid + kHistPerThread * kBlock; j < H; j += kBlock) add_hist(a.hist[h0 + j]);
+      for (uint32_t j = tid + kHistPerThread * kBlock; j < H; j += kBlock) add_hist(hr.at(j));
     }
     lds_signal(&L.misc[kSyncHist]);
   };
@@ -555,7 +570,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
     const uint32_t w = block_argmax(bv, bi, L.redv, L.redi);
     if (tid == 0) {
-      a.out_ids[b] = w == 0xffffffffu ? 0u : w;
+      store_result(a, b, w == 0xffffffffu ? 0u : w, len_b);
       if (a.out_kept) a.out_kept[b] = 0u;
     }
     return true;
@@ -751,11 +766,11 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // 7. The sequential tail (one wave).
   if (wave == 0) {
     if (K <= 64) {
-      draw_tail_bcast(a, b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u, u_draw,
-                      st_next, L.exptab, L.tail);
+      draw_tail_bcast(a, b, len_b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u,
+                      u_draw, st_next, L.exptab, L.tail);
     } else {
-      draw_tail(a, b, P, K, [&](uint32_t i) { return L.skey[i]; }, [&](uint32_t i) { return L.sid[i]; }, rng0,
-                L.exptab);
+      draw_tail(a, b, len_b, P, K, [&](uint32_t i) { return L.skey[i]; }, [&](uint32_t i) { return L.sid[i]; },
+                rng0, L.exptab);
     }
   }
   LLMHIP_MARK(8);

@@ -116,11 +116,20 @@ int validate(size_t B, size_t V, size_t ld, const float* logits, const llmhip_pa
 // Enqueue the kernels for one batch whose buffers are all on the device.
 // `params_host` is read on the host to choose kernels; `params_dev` is its
 // device copy (null when params_stride == 0).
+// Decode-step mode (ring-buffer histories); ring == null for a CSR history.
+struct RingArgs {
+  uint32_t* ring = nullptr;
+  uint32_t* ring_len = nullptr;
+  uint32_t* done = nullptr;
+  uint32_t cap = 0;
+  uint32_t window = 0;
+};
+
 int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
             const llmhip_params* params_host, size_t params_stride, const llmhip_params* params_dev,
             const uint32_t* hist, const uint32_t* hist_offsets, const uint8_t* allowed,
             size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
-            float* out_probs, uint32_t* out_kept, hipStream_t s) {
+            float* out_probs, uint32_t* out_kept, hipStream_t s, const RingArgs& ring = RingArgs()) {
   if (V == 0) {
     // Empty logits: sample_with returns 0 without drawing (generate.rs:375-377).
     HIP_TRY(hipMemsetAsync(out_ids, 0, B * sizeof(uint32_t), s));
@@ -152,8 +161,13 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.params = params_stride ? params_dev : nullptr;
   a.params_stride = (uint32_t)params_stride;
   a.shared = params_host[0];
-  a.hist = hist;
-  a.hist_offsets = hist_offsets;
+  a.hist = ring.ring ? ring.ring : hist;
+  a.hist_offsets = ring.ring ? nullptr : hist_offsets;
+  a.ring = ring.ring;
+  a.ring_len = ring.ring_len;
+  a.done = ring.done;
+  a.ring_cap = ring.cap;
+  a.window = ring.window;
   a.allowed = allowed_len ? allowed : nullptr;
   a.allowed_len = (uint32_t)allowed_len;
   a.eos_id = eos_id;
@@ -366,6 +380,33 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
     return LLMHIP_ERR_HIP;
   }
   return LLMHIP_OK;
+}
+
+int llmhip_decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                       const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
+                       uint32_t* ring_len, uint32_t* done, size_t window, const uint8_t* allowed,
+                       size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
+                       void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  int st = validate(B, V, ld, logits, params, nullptr, nullptr, allowed, allowed_len, rng_state, out_ids);
+  if (st || B == 0) return st;
+  if (!ring || !ring_len) return arg_fail("ring and ring_len are required");
+  if (ring_cap == 0 || ring_cap > 0x7fffffffu) return arg_fail("ring_cap must be in 1 .. 2^31-1");
+  if (window > ring_cap) return arg_fail("window must not exceed ring_cap");
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const llmhip_params* pdev = nullptr;
+  st = copy_params(ctx, params, B, params_stride, &pdev, s);
+  if (st) return st;
+  RingArgs r;
+  r.ring = ring;
+  r.ring_len = ring_len;
+  r.done = done;
+  r.cap = (uint32_t)ring_cap;
+  r.window = (uint32_t)window;
+  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, nullptr, nullptr, allowed, allowed_len,
+                 eos_id, rng_state, out_ids, nullptr, nullptr, s, r);
 }
 
 }  // extern "C"

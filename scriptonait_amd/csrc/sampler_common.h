@@ -59,6 +59,16 @@ struct SampleArgs {
   // by `allowed` (the fast kernel's layout, built by a prep kernel), or all
   // zeros when there is no mask. 1024 words, always valid.
   const uint32_t* slotmask;
+  // Decode-step mode (ring_cap > 0): row b's history is the last
+  // min(ring_len[b], window) tokens of the ring ring[b*ring_cap ..
+  // (b+1)*ring_cap) (hist == ring, hist_offsets == null); each result is
+  // appended to the ring (ring_len[b] += 1), or sets done[b] at eos_id, and
+  // rows with done[b] != 0 are skipped.
+  uint32_t* ring;
+  uint32_t* ring_len;
+  uint32_t* done;
+  uint32_t ring_cap;
+  uint32_t window;
   // Device word of kStatus* bits, set by a kernel that hit an internal
   // limit (zero after a correct call).
   uint32_t* status;
@@ -71,6 +81,52 @@ struct SampleArgs {
   uint64_t scratch_row_words;
   uint32_t row_class_mask;  // which row classes this launch handles
 };
+
+// Row b's history (`recent`, generate.rs:343-352): the CSR slice
+// hist[hist_offsets[b] .. hist_offsets[b+1]), or in decode-step mode the
+// last H = min(ring_len[b], window) tokens of row b's ring (the penalty only
+// counts occurrences, so the ring's order does not matter).
+struct HistRow {
+  const uint32_t* base;  // first id of the slice, or the row's ring
+  uint32_t start;        // ring: slot of the oldest token in the window
+  uint32_t cap;          // ring capacity (0 for a CSR slice)
+  uint32_t H;            // ids in the history
+  __device__ __forceinline__ uint32_t at(uint32_t j) const {
+    uint32_t k = start + j;
+    if (k >= cap && cap) k -= cap;
+    return base[k];
+  }
+};
+
+// v0, v1: hist_offsets[b], hist_offsets[b+1] (CSR) or ring_len[b] (ring).
+__device__ __forceinline__ HistRow hist_row(const SampleArgs& a, uint32_t b, uint32_t v0, uint32_t v1) {
+  HistRow h{a.hist, 0u, 0u, 0u};
+  if (a.ring_cap) {
+    h.cap = a.ring_cap;
+    h.H = min(v0, a.window);
+    h.base = a.ring + (size_t)b * a.ring_cap;
+    h.start = (v0 - h.H) % a.ring_cap;
+  } else if (a.hist && a.hist_offsets && v1 > v0) {
+    h.base = a.hist + v0;
+    h.H = v1 - v0;
+  }
+  return h;
+}
+
+// Row b's result: the id, and in decode-step mode the ring append (or the
+// end of the generation at eos_id, generate.rs:157-165). len_b is
+// ring_len[b] as the row read it.
+__device__ __forceinline__ void store_result(const SampleArgs& a, uint32_t b, uint32_t id, uint32_t len_b) {
+  a.out_ids[b] = id;
+  if (a.ring_cap) {
+    if (id == a.eos_id) {
+      if (a.done) a.done[b] = 1u;
+    } else {
+      a.ring[(size_t)b * a.ring_cap + len_b % a.ring_cap] = id;
+      a.ring_len[b] = len_b + 1u;
+    }
+  }
+}
 
 enum RowClass : uint32_t {
   kClassGreedy = 1u,  // temperature <= 0

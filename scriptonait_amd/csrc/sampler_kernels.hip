@@ -36,20 +36,31 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   const float* row = a.logits + (size_t)b * a.ld;
   if (tid < 32) L.exptab[tid] = exp2f_tab_lane(tid);
 
-  bool use_pen = P.repetition_penalty != 1.0f && a.hist && a.hist_offsets;
   uint32_t h0 = 0, h1 = 0;
-  if (use_pen) {
+  if (a.ring_cap) {
+    h0 = a.ring_len[b];
+    // Decode-step mode: a finished generation is skipped (no draw).
+    if (a.done && a.done[b]) {
+      if (tid == 0) {
+        a.out_ids[b] = a.eos_id;
+        if (a.out_kept) a.out_kept[b] = 0u;
+      }
+      return;
+    }
+  } else if (a.hist && a.hist_offsets) {
     h0 = a.hist_offsets[b];
     h1 = a.hist_offsets[b + 1];
-    use_pen = h1 > h0;
   }
+  const uint32_t len_b = h0;
+  const HistRow hr = hist_row(a, b, h0, h1);
+  const bool use_pen = P.repetition_penalty != 1.0f && hr.H > 0;
   if (use_pen) {
     // Integer multiplicities in L2 (device-scope atomics): order-independent.
     for (uint32_t i = tid; i < V; i += kBlock)
       __hip_atomic_store(&cnt[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    for (uint32_t j = h0 + tid; j < h1; j += kBlock) {
-      const uint32_t id = a.hist[j];
+    for (uint32_t j = tid; j < hr.H; j += kBlock) {
+      const uint32_t id = hr.at(j);
       if (id < V) atomicAdd(&cnt[id], 1u);
     }
     __syncthreads();
@@ -76,7 +87,7 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   if (greedy) {
     const uint32_t w = block_argmax(bv, bi, L.redv, L.redi);
     if (tid == 0) {
-      a.out_ids[b] = w == 0xffffffffu ? 0u : w;
+      store_result(a, b, w == 0xffffffffu ? 0u : w, len_b);
       if (a.out_kept) a.out_kept[b] = 0u;
     }
     return;
@@ -144,7 +155,7 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   // Four passes end in A.
   const uint32_t n = (P.top_k > 0 && P.top_k < V) ? P.top_k : V;
   if (wave == 0) {
-    draw_tail(a, b, P, n, [&](uint32_t i) { return keysA[i]; }, [&](uint32_t i) { return idsA[i]; },
+    draw_tail(a, b, len_b, P, n, [&](uint32_t i) { return keysA[i]; }, [&](uint32_t i) { return idsA[i]; },
               a.rng_state[b], L.exptab);
   }
 }

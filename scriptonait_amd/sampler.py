@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "llmhip_ctx_destroy",
     "llmhip_sample_host",
     "llmhip_sample_device",
+    "llmhip_decode_step",
 )
 
 
@@ -88,6 +89,8 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.llmhip_sample_host.argtypes = common
     lib.llmhip_sample_device.restype = ctypes.c_int
     lib.llmhip_sample_device.argtypes = common + [vp]
+    lib.llmhip_decode_step.restype = ctypes.c_int
+    lib.llmhip_decode_step.argtypes = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, sz, vp, sz, u32, vp, vp, vp]
     _lib = lib
     return lib
 
@@ -246,6 +249,29 @@ class Sampler:
             dp(hist), dp(hist_offsets), dp(allowed),
             0 if allowed is None else allowed.numel(), eos_id,
             dp(rng_state), dp(out_ids), dp(out_probs), dp(out_kept), stream.cuda_stream)
+        _check(self.lib, status)
+
+
+    def decode_step(self, logits, params: np.ndarray, ring, ring_len, done, window: int, rng_state, out_ids,
+                    V: Optional[int] = None, allowed=None, eos_id: int = EOS, stream=None) -> None:
+        """llmhip_decode_step on torch CUDA tensors: one Generator::step
+        (generate.rs:157-165) for B generations whose history ring
+        ([B, ring_cap] int32), lengths and done flags ([B] int32) and RNG
+        states ([B] int64 viewed as u64) live on the device. Enqueued on
+        `stream` (default: torch's current stream); does not synchronize."""
+        import torch
+
+        B, ld = logits.shape
+        V = ld if V is None else V
+        params = np.ascontiguousarray(params, dtype=PARAMS_DTYPE)
+        stride = 0 if params.shape[0] == 1 else 1
+        if stream is None:
+            stream = torch.cuda.current_stream(logits.device)
+        dp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        status = self.lib.llmhip_decode_step(
+            self.ctx, dp(logits), B, V, ld, _ptr(params), stride, dp(ring), ring.shape[1], dp(ring_len),
+            dp(done), window, dp(allowed), 0 if allowed is None else allowed.numel(), eos_id,
+            dp(rng_state), dp(out_ids), stream.cuda_stream)
         _check(self.lib, status)
 
 

@@ -14,7 +14,14 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def sampler():
-    """The GPU sampler. Fails (does not skip) when the library or GPU is missing."""
+    """The GPU sampler. Fails (does not skip) when the library or GPU is missing.
+
+    torch's HIP runtime (used by the device-buffer tests for allocation) is
+    brought up first, as bench.py does: it does not initialize after the
+    library's runtime has claimed the device in the same process."""
+    import torch
+
+    torch.cuda.init()
     from scriptonait_amd.sampler import Sampler
 
     s = Sampler(0)

@@ -1,0 +1,85 @@
+"""GPU: llmhip_decode_step against a CPU decode loop over the oracle.
+
+The loop is Generator::step (crates/llm-core/src/generate.rs:157-165) with
+recent_tokens (generate.rs:178-182): each step samples every live row with
+the last `window` tokens of its history (prompt included) as `recent`,
+appends the token, and ends the row at EOS. On the device the histories,
+lengths, done flags and RNG states stay in HBM across steps; on the CPU the
+same loop runs over Python lists with oracle.sample_batch. Every step's ids
+and the final rings, lengths, done flags and RNG states must match.
+"""
+import numpy as np
+import pytest
+
+from scriptonait_amd.workloads import EOS_ID, make_params
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3):
+    import torch
+
+    from oracle import oracle
+
+    rs = np.random.default_rng(seed)
+    dev = torch.device("cuda:0")
+    prompts = [rs.integers(0, V, size=int(rs.integers(1, 300))).astype(np.uint32) for _ in range(B)]
+    ring = np.zeros((B, cap), dtype=np.uint32)
+    for b, pr in enumerate(prompts):
+        for j, tok in enumerate(pr):
+            ring[b, j % cap] = tok
+    lens = np.array([len(p) for p in prompts], dtype=np.uint32)
+    rng0 = rs.integers(0, 2**63, size=B, dtype=np.uint64)
+    d_ring = torch.from_numpy(ring.view(np.int32)).to(dev)
+    d_len = torch.from_numpy(lens.view(np.int32)).to(dev)
+    d_done = torch.zeros(B, dtype=torch.int32, device=dev)
+    d_rng = torch.from_numpy(rng0.view(np.int64)).to(dev)
+    d_ids = torch.zeros(B, dtype=torch.int32, device=dev)
+    hist = [list(p) for p in prompts]
+    done = np.zeros(B, dtype=bool)
+    st = rng0.copy()
+    for t in range(steps):
+        logits = (rs.standard_normal((B, V)) * 3.0).astype(np.float32)
+        for b in range(B):  # some rows end at EOS along the way
+            if (b + 3 * t) % 29 == 0:
+                logits[b, EOS_ID] = 60.0
+        sampler.decode_step(torch.from_numpy(logits).to(dev), prm, d_ring, d_len, d_done, window, d_rng, d_ids)
+        live = np.nonzero(~done)[0]
+        want = np.full(B, EOS_ID, dtype=np.uint32)
+        if live.size:
+            recent = [np.array(hist[b][-window:], dtype=np.uint32) for b in live]
+            offs = np.concatenate([[0], np.cumsum([r.size for r in recent])]).astype(np.uint32)
+            o = oracle.sample_batch(logits[live], prm, st[live], np.concatenate(recent), offs, V=V)
+            want[live] = o.ids
+            st[live] = o.rng_state
+            for i, b in enumerate(live):
+                if o.ids[i] == EOS_ID:
+                    done[b] = True
+                else:
+                    hist[b].append(int(o.ids[i]))
+        got = d_ids.cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, want), (t, np.nonzero(got != want)[0])
+    assert done.any() and not done.all()
+    assert np.array_equal(d_done.cpu().numpy() != 0, done)
+    assert np.array_equal(d_rng.cpu().numpy().view(np.uint64), st)
+    glen = d_len.cpu().numpy().view(np.uint32)
+    assert np.array_equal(glen, [len(h) for h in hist])
+    gring = d_ring.cpu().numpy().view(np.uint32)
+    for b in range(B):
+        n = len(hist[b])
+        for j in range(max(0, n - cap), n):
+            assert gring[b, j % cap] == hist[b][j], (b, j)
+
+
+def test_decode_loop_top_k_path(sampler):
+    """Config-3 parameters, V = 32000 (the register path)."""
+    _run(sampler, 32000, make_params(0.7, 64, 0.95, 0.05, 1.15))
+
+
+def test_decode_loop_full_vocab_path(sampler):
+    """top_k = 0 (the sorting path), with a strong penalty and a short window."""
+    _run(sampler, 2048, make_params(1.0, 0, 0.9, 0.02, 1.8), window=16, cap=16)
+
+
+def test_decode_loop_greedy(sampler):
+    _run(sampler, 8192, make_params(0.0, 64, 0.95, 0.05, 1.3))
