@@ -14,6 +14,7 @@
 namespace llmhip {
 hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s);
 hipError_t launch_general(const SampleArgs& a, hipStream_t s);
+hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 }  // namespace llmhip
 
@@ -144,7 +145,10 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   }
   const bool fast_ok = V <= kMaxFastV;
   const uint32_t fast_mask = fast_ok ? (classes & (kClassGreedy | kClassTopK)) : 0u;
-  const uint32_t general_mask = classes & ~fast_mask;
+  // Full-vocabulary rows take the bucketed exact-fold kernel; it writes no
+  // out_probs, so a call that asks for them sorts those rows instead.
+  const uint32_t vocab_mask = out_probs ? 0u : (classes & kClassVocab);
+  const uint32_t general_mask = classes & ~fast_mask & ~vocab_mask;
 
   // The fast kernel may hand a row to the general path, so scratch is
   // always sized for the batch.
@@ -192,6 +196,10 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
     }
     a.row_class_mask = fast_mask;
     HIP_TRY(launch_fast(a, vec, s));
+  }
+  if (vocab_mask) {
+    a.row_class_mask = vocab_mask;
+    HIP_TRY(launch_vocab(a, s));
   }
   if (general_mask) {
     a.row_class_mask = general_mask;

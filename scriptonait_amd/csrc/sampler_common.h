@@ -131,7 +131,8 @@ __device__ __forceinline__ void store_result(const SampleArgs& a, uint32_t b, ui
 enum RowClass : uint32_t {
   kClassGreedy = 1u,  // temperature <= 0
   kClassTopK = 2u,    // 0 < top_k < V and top_k <= kMaxFastK
-  kClassFull = 4u,    // everything else (top_k == 0, top_k >= V, large top_k)
+  kClassFull = 4u,    // top_k > kMaxFastK and < V
+  kClassVocab = 8u,   // top_k == 0 or top_k >= V: the whole vocabulary is kept
 };
 
 constexpr uint32_t kStatusSyncTimeout = 1u;  // an LDS wait between waves ran out of spins
@@ -151,6 +152,7 @@ __host__ __device__ __forceinline__ uint32_t row_class(const llmhip_params& p, u
   // generate.rs:354: `temperature <= 0.0` (a NaN temperature is not greedy).
   if (p.temperature <= 0.0f) return kClassGreedy;
   if (p.top_k > 0 && p.top_k < V && p.top_k <= kMaxFastK) return kClassTopK;
+  if (p.top_k == 0 || p.top_k >= V) return kClassVocab;
   return kClassFull;
 }
 

@@ -15,6 +15,7 @@
 #include "draw_tail.h"
 #include "fast_row.h"
 #include "sampler_common.h"
+#include "vocab_row.h"
 #include "wave_ops.h"
 
 namespace llmhip {
@@ -169,6 +170,25 @@ __global__ __launch_bounds__(kBlock) void sample_general_kernel(SampleArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Full-vocabulary kernel (vocab_row.h); rows it cannot certify take the
+// sorting path in the same workgroup.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
+  __shared__ union {
+    VocabLds v;
+    GenLds gen;
+  } L;
+  const uint32_t b = blockIdx.x;
+  if (b >= a.B) return;
+  if (!(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  const bool vec4 = (reinterpret_cast<uintptr_t>(a.logits) % 16u == 0u) && (a.ld % 4u == 0u);
+  if (!vocab_row(a, b, L.v, vec4)) {
+    __syncthreads();
+    general_row(a, b, L.gen);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Fast path kernel.
 // ---------------------------------------------------------------------------
 template <int NCH, bool VEC>
@@ -230,6 +250,11 @@ hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s) {
     case 4: return launch_fast_nch<4>(a, vec, s);
     default: return launch_fast_nch<8>(a, vec, s);
   }
+}
+
+hipError_t launch_vocab(const SampleArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(sample_vocab_kernel, dim3(a.B), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_general(const SampleArgs& a, hipStream_t s) {

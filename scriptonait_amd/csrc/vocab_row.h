@@ -1,0 +1,815 @@
+// Full-vocabulary rows (top_k == 0 or top_k >= V, temperature > 0) without
+// sorting the row.
+//
+// crates/llm-core/src/generate.rs:364-419 sorts the whole row by (value
+// desc, id asc) and then runs three f32 left folds in that order: the softmax
+// sum (374), the top-p cumulative (397-409; its value at the cut is also the
+// total of 411) and the inverse-CDF walk (412-419). This path produces the
+// same results, bit for bit, from two facts:
+//
+//  * x = expf(w - max) is monotone in w (glibc's expf is monotone on
+//    (-inf, 0]; checked exhaustively), and so is p = x / S. Each fold is
+//    therefore a fold over a multiset of values taken in descending order.
+//  * While a fold's running value F stays in one binade [2^E, 2^(E+1)),
+//    fl(F + t) = F + rne(t / u) * u with u = 2^(E-23): an integer count of
+//    ulps that does not depend on where t comes in the order, except at an
+//    exact half-ulp tie, where round-half-even looks at the parity of F.
+//
+// The row is bucketed by y = w - max, 128 buckets per unit of y (bucket 0
+// holds the max). An approximate prefix of the buckets' masses shows which
+// buckets may hold a binade crossing or a stop (the top-p cut, the walk's
+// pick). Those "zones" are gathered into LDS, sorted, and replayed 64
+// elements at a time in integer ulps, with the elements where something
+// happens (a crossing, a stop, a tie) stepped in f32. Every other
+// ("certain") bucket adds its exact integer ulp count with LDS atomics, and
+// the certain runs between zones are added as integers. A certain bucket
+// that holds a tie is split at the tie: a second sweep sums the ulp counts of
+// the bucket's elements that come before each tie, and the replay applies
+// round-half-even to the tie with the parity it then knows.
+//
+// Every assumption the approximate prefix made is checked exactly during the
+// replay; a row whose check fails, or that needs more zones than the LDS
+// holds, is handed to the sorting path (general_row), so the ids are the
+// reference's either way.
+//
+// Each pass streams the row again (the re-reads of a row that a CU has just
+// read come from the MALL).
+#pragma once
+#include "draw_tail.h"
+#include "fast_row.h"
+#include "sampler_common.h"
+#include "wave_ops.h"
+
+namespace llmhip {
+
+constexpr uint32_t kVB = 4096;             // buckets
+constexpr float kVR = 128.0f;              // buckets per unit of y
+constexpr uint32_t kVZones = 320;          // zones per fold
+constexpr uint32_t kVZoneEls = 4096;       // gathered elements per fold
+constexpr uint32_t kVTies = 256;           // ties in certain buckets per fold
+constexpr uint32_t kVHash = 2048;          // repetition-count table slots
+constexpr uint32_t kVMaxDistinct = 1536;   // distinct history ids the table takes
+constexpr uint32_t kVBits = 4096;          // words of the history filter (bit id mod 2^17)
+constexpr uint32_t kHashEmpty = 0xffffffffu;
+constexpr int32_t kNoE = -1000;            // segment without certain buckets
+constexpr uint32_t kNoPos = 0xffffffffu;
+
+enum : uint8_t { kBSkip = 0, kBCert = 1, kBZone = 2, kBTie = 3 };
+
+// misc[] slots
+enum : uint32_t {
+  kVFail = 0,      // nonzero: hand the row to general_row
+  kVBeyond = 1,    // first bucket certain to lie past a stop
+  kVNTies = 2,     // ties found in certain buckets
+  kVCount = 3,     // terms >= the min-p threshold
+  kVStopPos = 4,   // fold results
+  kVStopId = 5,
+  kVStopBk = 6,
+  kVF = 7,
+  kVDistinct = 8,  // distinct history ids
+  kVMisc = 9,
+};
+
+struct VocabLds {
+  uint32_t cnt[kVB];   // elements per bucket
+  float asum[kVB];     // approximate sum of x per bucket
+  uint32_t D[kVB];     // exact ulp counts of a fold's certain buckets
+  uint16_t zs[kVB];    // zone slot (zones) or segment index (certain buckets)
+  uint8_t cls[kVB];
+  // Zones in bucket order; segment z holds the certain buckets before zone z.
+  uint32_t zb[kVZones];
+  uint32_t zbase[kVZones + 1];
+  uint32_t zcur[kVZones];
+  uint32_t zpos[kVZones];       // sorted position of the zone bucket's first element
+  int32_t zE[kVZones];          // tie zones: the bucket's binade
+  uint32_t zTub[kVZones];       // tie zones: largest term of the bucket (walk)
+  uint16_t zt0[kVZones];        // tie zones: first tie (sorted tie order), count
+  uint16_t ztn[kVZones];
+  unsigned long long seg[kVZones + 1];
+  int32_t segE[kVZones + 1];
+  uint32_t segTub[kVZones + 1];  // largest term bound of the segment (walk)
+  // Gathered zone elements and their sorted order. Before the first fold,
+  // zkey/zid hold the buckets' masses as 64-bit fixed point (amass).
+  alignas(8) uint32_t zkey[kVZoneEls];
+  uint32_t zid[kVZoneEls];
+  uint16_t zperm[kVZoneEls];
+  // Ties in certain buckets: key, id, ulp count, bucket; ulp sum above each.
+  uint32_t tkey[kVTies], tidx[kVTies], tq[kVTies], tbk[kVTies], tab[kVTies];
+  uint16_t tord[kVTies];
+  uint32_t hkey[kVHash];
+  float hval[kVHash];
+  uint32_t hbits[kVBits];  // set for every history id (mod 2^17): the table is probed only then
+  double scand[kWaves];
+  uint32_t scanu[kWaves];
+  float redf[kWaves];
+  uint32_t misc[kVMisc];
+  uint64_t exptab[32];
+};
+
+__device__ __forceinline__ uint32_t vbucket(float y) {
+  const float ny = -y;
+  return ny < 32.0f ? (uint32_t)(ny * kVR) : kVB - 1u;
+}
+
+// Binade of a positive normal double.
+__device__ __forceinline__ int dbinade(double v) {
+  return (int)((uint64_t)(__double_as_longlong(v) >> 52) & 0x7ffu) - 1023;
+}
+
+__device__ __forceinline__ float from_units(uint32_t M, int E) {
+  return __uint_as_float(((uint32_t)(E + 127) << 23) | (M & 0x7fffffu));
+}
+
+// t >= 0 in units of 2^(E-23), rounded to nearest; tie: exactly half-way
+// (the result is then the lower neighbour). big: t >= 2^E, which a certain
+// bucket never holds.
+__device__ __forceinline__ uint32_t rne_units(float t, int E, bool& tie, bool& big) {
+  const uint32_t u = __float_as_uint(t);
+  const uint32_t ef = (u >> 23) & 255u;
+  const uint32_t m = ef ? ((u & 0x7fffffu) | 0x800000u) : (u & 0x7fffffu);
+  const int s = E - (ef ? (int)ef - 127 : -126);
+  tie = false;
+  big = s <= 0;
+  if (s <= 0 || s >= 25) return 0u;
+  const uint32_t q = m >> s, rem = m & ((1u << s) - 1u), half = 1u << (s - 1);
+  tie = rem == half;
+  return q + (rem > half ? 1u : 0u);
+}
+
+// Exclusive prefix over the workgroup; total gets the sum. All threads call.
+__device__ __forceinline__ uint32_t block_scan_u32(uint32_t x, uint32_t* tmp, uint32_t& total) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t inc = wave_incl_scan(x);
+  if (lane == 63u) tmp[wave] = inc;
+  __syncthreads();
+  const uint32_t wv = lane < kWaves ? tmp[lane] : 0u;
+  const uint32_t winc = wave_incl_scan(wv);
+  total = readlane_u32(winc, kWaves - 1u);
+  const uint32_t base = readlane_u32(winc - wv, wave);
+  __syncthreads();
+  return base + inc - x;
+}
+__device__ __forceinline__ double block_scan_f64(double x, double* tmp, double& total) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const double inc = wave_incl_scan_f64(x);
+  if (lane == 63u) tmp[wave] = inc;
+  __syncthreads();
+  const double wv = lane < kWaves ? tmp[lane] : 0.0;
+  const double winc = wave_incl_scan_f64(wv);
+  total = readlane_f64(winc, kWaves - 1u);
+  const double base = readlane_f64(winc - wv, wave);
+  __syncthreads();
+  return base + (inc - x);
+}
+
+// Element source: for_each(f) calls f(w, id) once for every element of the
+// row, w being the masked, penalized logit divided by the temperature.
+// Row streamed from memory by every pass: float4 groups, two batches of 4
+// per thread in flight (the next batch loads while this one is visited), or
+// scalars when the row is not 16-byte aligned.
+template <class WV>
+struct StreamSrc {
+  const float* row;
+  uint32_t V;
+  bool vec4;
+  WV wval;
+  template <class F>
+  __device__ __forceinline__ void for_each(F&& f) const {
+    if (vec4) {
+      const float4* r4 = reinterpret_cast<const float4*>(row);
+      const uint32_t nq = (V + 3u) / 4u;
+      float4 cur[4], nxt[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t q = threadIdx.x + kBlock * s;
+        cur[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      for (uint32_t q0 = 0; q0 < nq; q0 += 4u * kBlock) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const uint32_t q = q0 + 4u * kBlock + threadIdx.x + kBlock * s;
+          nxt[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const uint32_t i = 4u * (q0 + threadIdx.x + kBlock * s);
+          const float v[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (i + c < V) f(wval(i + c, v[c]), i + c);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) cur[s] = nxt[s];
+      }
+    } else {
+      uint32_t i = threadIdx.x;
+      for (; i + 7u * kBlock < V; i += 8u * kBlock) {
+        float v[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) v[s] = row[i + kBlock * s];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) f(wval(i + kBlock * s, v[s]), i + kBlock * s);
+      }
+      for (; i < V; i += kBlock) f(wval(i, row[i]), i);
+    }
+  }
+};
+
+// One fold over the row's terms in sorted order (see the file comment).
+struct FoldSpec {
+  float F0;          // starting value
+  float S;           // terms are x / S (0: the terms are x)
+  float thr;         // terms below thr are outside the fold (min-p); <= 0: none
+  float stop_ge;     // add folds: stop at the first F >= stop_ge
+  uint32_t kend;     // buckets >= kend are outside the fold
+  uint32_t kpart;    // bucket whose positions >= pos_end are outside (or kVB)
+  uint32_t pos_end;  // sorted positions >= pos_end are outside
+  bool sub;          // the walk: stop before t when F < t, else F -= t
+};
+
+struct FoldRes {
+  float F;
+  uint32_t stop_pos;  // kNoPos: no stop
+  uint32_t stop_id;
+  uint32_t stop_bk;
+};
+
+// (key desc, id asc): the reference's order (generate.rs:364-367).
+__device__ __forceinline__ bool before(uint32_t ka, uint32_t ia, uint32_t kb, uint32_t ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+template <class Src>
+__device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds& L, const Src& src, FoldRes& res) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t k0 = tid * 4u;
+  const double scale = fs.S > 0.0f ? 1.0 / (double)fs.S : 1.0;
+  auto term_of = [&](float x) __attribute__((always_inline)) { return fs.S > 0.0f ? x / fs.S : x; };
+
+  for (uint32_t s = tid; s <= kVZones; s += kBlock) {
+    L.seg[s] = 0ull;
+    L.segE[s] = kNoE;
+    L.segTub[s] = 0u;
+  }
+  if (tid == 0) {
+    L.misc[kVBeyond] = kVB;
+    L.misc[kVNTies] = 0u;
+    L.misc[kVCount] = 0u;
+  }
+
+  // Classification of this thread's 4 buckets from the approximate prefix.
+  // The margin is 6 sigma of a random walk of half-ulp rounding errors plus
+  // 2^-20 of the value for the approximate masses; the replay checks every
+  // consequence exactly, so a wrong guess costs a hand-over, not an id.
+  uint32_t c4[4];
+  double a4[4];
+  float tub4[4];
+  uint8_t cl[4];
+  int e4[4] = {0, 0, 0, 0};
+  uint32_t cs = 0;
+  double as = 0.0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t k = k0 + j;
+    c4[j] = L.cnt[k];
+    tub4[j] = term_of(glibc_expf_tab(-(float)k / kVR, L.exptab));
+    const bool out = !c4[j] || k >= fs.kend || (fs.thr > 0.0f && tub4[j] < fs.thr);
+    a4[j] = out ? 0.0 : (double)L.asum[k] * scale;
+    cl[j] = out ? kBSkip : kBCert;
+    cs += c4[j];
+    as += a4[j];
+  }
+  uint32_t ctot;
+  const uint32_t cpre = block_scan_u32(cs, L.scanu, ctot);
+  double atot;
+  const double apre = block_scan_f64(as, L.scand, atot);
+  {
+    const double sg = fs.sub ? -1.0 : 1.0;
+    uint32_t nb = cpre;
+    double P = apre;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t k = k0 + j;
+      const double Ga = fs.F0 + sg * P, Gb = fs.F0 + sg * (P + a4[j]);
+      if (cl[j] != kBSkip) {
+        const float tlb = k + 1 < kVB ? term_of(glibc_expf_tab(-(float)(k + 1) / kVR, L.exptab)) : 0.0f;
+        if (k == 0 || k == fs.kpart || (fs.thr > 0.0f && tlb < fs.thr)) {
+          cl[j] = kBZone;
+        } else {
+          double hi = fmax(Ga, Gb), lo = fmin(Ga, Gb);
+          const double err = (6.0 * sqrt((double)nb + 1.0) * 0x1p-24 + 0x1p-20) * (fs.sub ? (double)fs.F0 : hi);
+          if ((!fs.sub && Ga - err >= (double)fs.stop_ge) || (fs.sub && Ga + err < 0.0)) {
+            cl[j] = kBSkip;
+            atomicMin(&L.misc[kVBeyond], k);
+          } else {
+            lo -= err;
+            hi += err;
+            const int E = lo > 0.0 ? dbinade(lo) : 0;
+            if (!(lo > 0.0) || E != dbinade(hi) || E < -120 || E > 120 || (!fs.sub && hi >= (double)fs.stop_ge) ||
+                (fs.sub && lo <= (double)tub4[j] * (1.0 + 0x1p-20))) {
+              cl[j] = kBZone;
+            } else {
+              e4[j] = E;
+            }
+          }
+        }
+      }
+      nb += c4[j];
+      P += a4[j];
+    }
+  }
+  __syncthreads();
+  const uint32_t kb = L.misc[kVBeyond];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (k0 + j >= kb) cl[j] = kBSkip;
+
+  // Zone slots, segment indices and element bases, in bucket order. Run a
+  // second time when ties made certain buckets into tie zones: those hold no
+  // elements, so every gathering zone keeps its element base, and its
+  // gathered count is carried over in D[bucket].
+  uint32_t nz = 0;
+  auto layout = [&](bool again) __attribute__((always_inline)) -> bool {
+    uint32_t zc = 0, ze = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      zc += (cl[j] == kBZone || cl[j] == kBTie) ? 1u : 0u;
+      ze += cl[j] == kBZone ? c4[j] : 0u;
+    }
+    uint32_t nel;
+    uint32_t zi = block_scan_u32(zc, L.scanu, nz);
+    uint32_t ei = block_scan_u32(ze, L.scanu, nel);
+    if (nz > kVZones || nel > kVZoneEls) return false;
+    uint32_t pos = cpre;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t k = k0 + j;
+      if (cl[j] == kBZone || cl[j] == kBTie) {
+        L.zs[k] = (uint16_t)zi;
+        L.zb[zi] = k;
+        L.zbase[zi] = ei;
+        L.zcur[zi] = again && cl[j] == kBZone ? L.D[k] : 0u;
+        L.zpos[zi] = pos;
+        L.zE[zi] = e4[j];
+        L.zTub[zi] = __float_as_uint(tub4[j]);
+        ++zi;
+        if (cl[j] == kBZone) ei += c4[j];
+      } else if (cl[j] == kBCert) {
+        L.zs[k] = (uint16_t)zi;
+        L.segE[zi] = e4[j];
+        atomicMax(&L.segTub[zi], __float_as_uint(tub4[j]));
+      }
+      L.cls[k] = cl[j];
+      pos += c4[j];
+    }
+    if (tid == 0) L.zbase[nz] = nel;
+    return true;
+  };
+  if (!layout(false)) return false;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) L.D[k0 + j] = 0u;
+  __syncthreads();
+
+  // Exact pass: certain buckets add ulp counts, zones gather, ties are listed.
+  uint32_t nin = 0;
+  src.for_each([&](float w, uint32_t i) __attribute__((always_inline)) {
+    const float y = w - mx;
+    const uint32_t k = vbucket(y);
+    const uint8_t c = L.cls[k];
+    if (c == kBSkip) return;
+    const float t = term_of(glibc_expf_tab(y, L.exptab));
+    if (fs.thr > 0.0f && !(t >= fs.thr)) return;
+    ++nin;
+    if (c == kBZone) {
+      const uint32_t z = L.zs[k];
+      const uint32_t e = L.zbase[z] + atomicAdd(&L.zcur[z], 1u);
+      L.zkey[e] = f2key(w);
+      L.zid[e] = i;
+    } else {
+      bool tie, big;
+      const uint32_t q = rne_units(t, L.segE[L.zs[k]], tie, big);
+      if (big) L.misc[kVFail] = 1u;
+      if (tie) {
+        const uint32_t s = atomicAdd(&L.misc[kVNTies], 1u);
+        if (s < kVTies) {
+          L.tkey[s] = f2key(w);
+          L.tidx[s] = i;
+          L.tq[s] = q;
+          L.tbk[s] = k;
+          L.tab[s] = 0u;
+        }
+      } else {
+        atomicAdd(&L.D[k], q);
+      }
+    }
+  });
+  nin = wave_sum(nin);
+  if (lane == 0) atomicAdd(&L.misc[kVCount], nin);
+  __syncthreads();
+  const uint32_t nt = L.misc[kVNTies];
+  if (L.misc[kVFail] || nt > kVTies) return false;
+
+  if (nt) {
+    // Ties in certain buckets: sort them by (bucket, key desc, id asc), make
+    // their buckets tie zones, and sum each bucket's ulp counts above each
+    // tie.
+    for (uint32_t s = tid; s < nt; s += kBlock) {
+      uint32_t r = 0;
+      const uint32_t bs = L.tbk[s], ks = L.tkey[s], is = L.tidx[s];
+      for (uint32_t u = 0; u < nt; ++u) {
+        const uint32_t bu = L.tbk[u];
+        r += (bu < bs || (bu == bs && before(L.tkey[u], L.tidx[u], ks, is))) ? 1u : 0u;
+      }
+      L.tord[r] = (uint16_t)s;
+    }
+    for (uint32_t s = tid; s < nt; s += kBlock) L.cls[L.tbk[s]] = kBTie;
+    for (uint32_t z = tid; z < nz; z += kBlock)
+      if (L.cls[L.zb[z]] == kBZone) L.D[L.zb[z]] = L.zcur[z];
+    for (uint32_t s = tid; s <= kVZones; s += kBlock) {
+      L.segE[s] = kNoE;
+      L.segTub[s] = 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (L.cls[k0 + j] == kBTie) cl[j] = kBTie;
+    if (!layout(true)) return false;
+    __syncthreads();
+    for (uint32_t z = tid; z < nz; z += kBlock) {
+      const uint32_t k = L.zb[z];
+      if (L.cls[k] != kBTie) continue;
+      uint32_t lo = 0, hi = nt;  // the bucket's ties are a run of tord
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (L.tbk[L.tord[mid]] < k) lo = mid + 1; else hi = mid;
+      }
+      uint32_t e = lo;
+      while (e < nt && L.tbk[L.tord[e]] == k) ++e;
+      L.zt0[z] = (uint16_t)lo;
+      L.ztn[z] = (uint16_t)(e - lo);
+    }
+    __syncthreads();
+    src.for_each([&](float w, uint32_t i) __attribute__((always_inline)) {
+      const float y = w - mx;
+      const uint32_t k = vbucket(y);
+      if (L.cls[k] != kBTie) return;
+      const float t = term_of(glibc_expf_tab(y, L.exptab));
+      if (fs.thr > 0.0f && !(t >= fs.thr)) return;
+      const uint32_t z = L.zs[k];
+      bool tie, big;
+      const uint32_t q = rne_units(t, L.zE[z], tie, big);
+      if (tie || q == 0u) return;
+      const uint32_t key = f2key(w);
+      const uint32_t t0 = L.zt0[z], tn = L.ztn[z];
+      for (uint32_t u = 0; u < tn; ++u) {
+        const uint32_t s = L.tord[t0 + u];
+        if (before(key, i, L.tkey[s], L.tidx[s])) atomicAdd(&L.tab[s], q);
+      }
+    });
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (cl[j] == kBCert) atomicAdd(&L.seg[L.zs[k0 + j]], (unsigned long long)L.D[k0 + j]);
+
+  // Sort each gathering zone by (key desc, id asc): rank by counting.
+  for (uint32_t z = wave; z < nz; z += kWaves) {
+    if (L.cls[L.zb[z]] != kBZone) continue;
+    const uint32_t base = L.zbase[z], n = L.zcur[z];
+    for (uint32_t i = lane; i < n; i += 64u) {
+      const uint32_t ki = L.zkey[base + i], ii = L.zid[base + i];
+      uint32_t r = 0;
+      for (uint32_t j = 0; j < n; ++j) r += before(L.zkey[base + j], L.zid[base + j], ki, ii) ? 1u : 0u;
+      L.zperm[base + r] = (uint16_t)i;
+    }
+  }
+  __syncthreads();
+
+  // Replay (wave 0): certain segments as integers, tie zones split at their
+  // ties, gathering zones 64 elements at a time.
+  if (wave == 0) {
+    float F = fs.F0;
+    bool fail = false, stopped = false;
+    uint32_t stop_pos = kNoPos, stop_id = 0, stop_bk = 0;
+    // Adds d ulps to F in binade E (add folds) or takes them away (the walk);
+    // false when F would leave the binade.
+    auto apply_units = [&](int E, uint64_t d) __attribute__((always_inline)) -> bool {
+      const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
+      if (!(F > 0.0f) || ef == 0u || ef == 255u || (int)ef - 127 != E) return false;
+      uint64_t M = (fb & 0x7fffffu) | 0x800000u;
+      if (!fs.sub) {
+        M += d;
+        if (M >= (1ull << 24)) return false;
+      } else {
+        if (M < d + (1ull << 23) + 1ull) return false;
+        M -= d;
+      }
+      F = from_units((uint32_t)M, E);
+      return true;
+    };
+    // One element in f32, the reference's way; true when the fold stops.
+    auto step = [&](float tv) __attribute__((always_inline)) -> bool {
+      if (fs.sub) {
+        if (F < tv) return true;
+        F = F - tv;
+        return false;
+      }
+      F = F + tv;
+      return F >= fs.stop_ge;
+    };
+    for (uint32_t z = 0; z <= nz && !fail && !stopped; ++z) {
+      const int Es = L.segE[z];
+      if (Es != kNoE) {
+        if (!apply_units(Es, L.seg[z])) fail = true;
+        else if (!fs.sub && F >= fs.stop_ge) fail = true;
+        else if (fs.sub && F < __uint_as_float(L.segTub[z])) fail = true;
+      }
+      if (z == nz || fail) break;
+      const uint32_t k = L.zb[z];
+      if (L.cls[k] == kBTie) {
+        const int E = L.zE[z];
+        uint32_t prev = 0;
+        const uint32_t t0 = L.zt0[z], tn = L.ztn[z];
+        for (uint32_t u = 0; u < tn && !fail; ++u) {
+          const uint32_t s = L.tord[t0 + u];
+          const uint32_t ab = L.tab[s];
+          if (!apply_units(E, ab - prev)) fail = true;
+          prev = ab;
+          const uint32_t q = L.tq[s];
+          const uint32_t par = (__float_as_uint(F) ^ q) & 1u;  // parity of M - q or M + q
+          if (!fail && !apply_units(E, (uint64_t)q + par)) fail = true;
+        }
+        if (!fail && !apply_units(E, L.D[k] - prev)) fail = true;
+        if (!fail && !fs.sub && F >= fs.stop_ge) fail = true;
+        if (!fail && fs.sub && F < __uint_as_float(L.zTub[z])) fail = true;
+        continue;
+      }
+      const uint32_t base = L.zbase[z], n = L.zcur[z], p0 = L.zpos[z];
+      uint32_t r0 = 0;
+      while (r0 < n && !stopped) {
+        const uint32_t r = r0 + lane;
+        float t = 0.0f;
+        uint32_t id = 0u;
+        if (r < n) {  // the term again, as the exact pass made it
+          const uint32_t e = base + L.zperm[base + r];
+          t = term_of(glibc_expf_tab(key2f(L.zkey[e]) - mx, L.exptab));
+          id = L.zid[e];
+        }
+        const bool live = r < n;
+        const bool past = live && p0 + r >= fs.pos_end;
+        const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
+        uint32_t ev_lane = 0u;  // first lane stepped in f32
+        uint32_t done = 0u;     // lanes before it, folded as integers
+        if (F > 0.0f && ef >= 1u && ef <= 254u) {
+          const int E = (int)ef - 127;
+          const uint32_t M = (fb & 0x7fffffu) | 0x800000u;
+          bool tie = false, big = false;
+          const uint32_t q = live && !past ? rne_units(t, E, tie, big) : 0u;
+          const uint32_t incl = wave_incl_scan(q), excl = incl - q;
+          bool ev;
+          if (!fs.sub) {
+            const uint64_t Mi = (uint64_t)M + incl;
+            ev = tie || big || Mi >= (1ull << 24) || from_units((uint32_t)Mi, E) >= fs.stop_ge;
+          } else {
+            const bool ub = (uint64_t)excl + (1ull << 23) + 1ull > M;
+            const bool ui = (uint64_t)incl + (1ull << 23) + 1ull > M;
+            ev = tie || big || ub || ui || from_units(M - excl, E) < t;
+          }
+          ev = live && (ev || past);
+          const uint64_t m = __ballot(ev);
+          ev_lane = m ? (uint32_t)__ffsll((unsigned long long)m) - 1u : 64u;
+          done = min(ev_lane, n - r0);
+          if (done) {
+            const uint32_t sum = readlane_u32(incl, done - 1u);
+            const uint64_t M2 = fs.sub ? (uint64_t)M - sum : (uint64_t)M + sum;
+            F = from_units((uint32_t)M2, E);
+          }
+        }
+        if (r0 + done >= n) {
+          r0 = n;
+          break;
+        }
+        if (done == 64u) {  // no event in these 64
+          r0 += 64u;
+          continue;
+        }
+        // Element ev_lane (or the first one when F is not a normal number).
+        const uint32_t le = done;
+        const uint32_t pos = p0 + r0 + le;
+        if (pos >= fs.pos_end) {
+          stopped = true;  // the rest of the fold is outside it
+          break;
+        }
+        if (step(readlane_f32(t, le))) {
+          stop_pos = pos;
+          stop_id = readlane_u32(id, le);
+          stop_bk = k;
+          stopped = true;
+          break;
+        }
+        r0 += le + 1u;
+      }
+    }
+    // Past the end without a stop, although a bucket was certain to lie
+    // past the stop: the approximation was wrong.
+    if (!fail && stop_pos == kNoPos && kb < kVB) fail = true;
+    if (lane == 0) {
+      L.misc[kVFail] = fail ? 1u : 0u;
+      L.misc[kVStopPos] = stop_pos;
+      L.misc[kVStopId] = stop_id;
+      L.misc[kVStopBk] = stop_bk;
+      L.misc[kVF] = __float_as_uint(F);
+    }
+  }
+  __syncthreads();
+  res.F = __uint_as_float(L.misc[kVF]);
+  res.stop_pos = L.misc[kVStopPos];
+  res.stop_id = L.misc[kVStopId];
+  res.stop_bk = L.misc[kVStopBk];
+  const bool ok = L.misc[kVFail] == 0u;
+  __syncthreads();
+  return ok;
+}
+
+// The three folds and the draw, given the row's source. Returns false
+// (uniformly) when the row must go to general_row.
+template <class Src>
+__device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uint32_t len_b, const llmhip_params& P, VocabLds& L,
+                            const Src& src) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t V = a.V;
+  // Max; NaN and +inf rows take the sorting path.
+  float mx = -INFINITY;
+  uint32_t bad = 0u;
+  src.for_each([&](float w, uint32_t) __attribute__((always_inline)) {
+    if (w != w || w == INFINITY) bad = 1u;
+    mx = fmaxf(mx, w);
+  });
+#pragma unroll
+  for (uint32_t off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (__ballot(bad != 0u) && lane == 0) L.misc[kVFail] = 1u;
+  if (lane == 0) L.redf[wave] = mx;
+  for (uint32_t k = tid; k < kVB; k += kBlock) {
+    L.cnt[k] = 0u;
+    L.asum[k] = 0.0f;
+  }
+  __syncthreads();
+  mx = L.redf[0];
+  for (uint32_t w = 1; w < kWaves; ++w) mx = fmaxf(mx, L.redf[w]);
+  if (L.misc[kVFail] || mx == -INFINITY) return false;
+
+  // Bucket counts and approximate masses. The masses add up as integers
+  // (x in units of 2^-40): LDS integer atomics are much faster than float ones.
+  static_assert(sizeof(L.zkey) + sizeof(L.zid) >= kVB * sizeof(unsigned long long), "amass");
+  unsigned long long* amass = reinterpret_cast<unsigned long long*>(L.zkey);
+  for (uint32_t k = tid; k < kVB; k += kBlock) amass[k] = 0ull;
+  __syncthreads();
+  src.for_each([&](float w, uint32_t) __attribute__((always_inline)) {
+    const float y = w - mx;
+    const uint32_t k = vbucket(y);
+    atomicAdd(&L.cnt[k], 1u);
+    const uint32_t xb = __float_as_uint(__expf(y));
+    const int sh = (int)((xb >> 23) & 255u) - 127 + 17;  // x * 2^40 = m * 2^(e + 17)
+    const unsigned long long m = (xb & 0x7fffffu) | 0x800000u;
+    const unsigned long long fx = sh >= 0 ? (m << sh) : (sh > -24 ? (m >> -sh) : 0ull);
+    if (fx) atomicAdd(&amass[k], fx);
+  });
+  __syncthreads();
+  for (uint32_t k = tid; k < kVB; k += kBlock) L.asum[k] = (float)((double)amass[k] * 0x1p-40);
+  __syncthreads();
+
+  // generate.rs:372-377: the softmax sum. The max element has x = 1, so S >= 1.
+  FoldRes r;
+  FoldSpec fs{0.0f, 0.0f, 0.0f, INFINITY, kVB, kVB, kNoPos, false};
+  if (!run_fold(fs, mx, L, src, r)) return false;
+  const float S = r.F;
+  if (!(S > 0.0f) || !isfinite(S)) return false;
+
+  // generate.rs:378-409: p = x / S; min-p by value (p is monotone along the
+  // order); the top-p cumulative, whose value at the cut is the total.
+  const float p0 = 1.0f / S;
+  const float thr = P.min_p > 0.0f ? P.min_p * p0 : 0.0f;
+  fs = FoldSpec{0.0f, S, thr, P.top_p < 1.0f ? P.top_p : INFINITY, kVB, kVB, kNoPos, false};
+  if (!run_fold(fs, mx, L, src, r)) return false;
+  const bool cut = r.stop_pos != kNoPos;
+  uint32_t keep;
+  if (cut) {
+    keep = r.stop_pos + 1u;
+  } else if (P.min_p > 0.0f) {
+    keep = max(1u, L.misc[kVCount]);
+  } else {
+    keep = V;
+  }
+  const float total = r.F;
+  const uint32_t cut_id = r.stop_id, cut_bk = r.stop_bk;
+
+  // generate.rs:411-419: r = u * total, then the walk.
+  uint64_t st = a.rng_state[b];
+  const float u = next_f32(st);
+  const float r0 = u * total;
+  fs = FoldSpec{r0, S, thr, INFINITY, cut ? cut_bk + 1u : kVB, cut ? cut_bk : kVB, keep, true};
+  if (!run_fold(fs, mx, L, src, r)) return false;
+  uint32_t pick;
+  if (r.stop_pos != kNoPos) {
+    pick = r.stop_id;
+  } else if (cut) {
+    pick = cut_id;  // order[keep - 1]
+  } else {
+    return false;
+  }
+  if (tid == 0) {
+    store_result(a, b, pick, len_b);
+    a.rng_state[b] = st;
+    if (a.out_kept) a.out_kept[b] = keep;
+  }
+  return true;
+}
+
+// Returns false (uniformly) when the row must go to general_row.
+__device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, VocabLds& L, bool vec4) {
+  const uint32_t tid = threadIdx.x;
+  const llmhip_params P = load_params(a, b);
+  const uint32_t V = a.V;
+  const float* row = a.logits + (size_t)b * a.ld;
+  if (tid < 32) L.exptab[tid] = exp2f_tab_lane(tid);
+  if (tid < kVMisc) L.misc[tid] = 0u;
+
+  uint32_t h0 = 0, h1 = 0;
+  if (a.ring_cap) {
+    h0 = a.ring_len[b];
+    if (a.done && a.done[b]) {
+      if (tid == 0) {
+        a.out_ids[b] = a.eos_id;
+        if (a.out_kept) a.out_kept[b] = 0u;
+      }
+      return true;
+    }
+  } else if (a.hist && a.hist_offsets) {
+    h0 = a.hist_offsets[b];
+    h1 = a.hist_offsets[b + 1];
+  }
+  const uint32_t len_b = h0;
+  const HistRow hr = hist_row(a, b, h0, h1);
+  const float rp = P.repetition_penalty, T = P.temperature;
+  const bool use_pen = rp != 1.0f && hr.H > 0;
+  __syncthreads();
+
+  // Repetition counts in an LDS hash (open addressing, probes bounded by the
+  // table size), then each history id's penalized value (generate.rs:333-352:
+  // the mask first, then one penalty step per occurrence).
+  if (use_pen) {
+    for (uint32_t s = tid; s < kVHash; s += kBlock) {
+      L.hkey[s] = kHashEmpty;
+      L.D[s] = 0u;
+    }
+    for (uint32_t s = tid; s < kVBits; s += kBlock) L.hbits[s] = 0u;
+    __syncthreads();
+    for (uint32_t j = tid; j < hr.H; j += kBlock) {
+      const uint32_t id = hr.at(j);
+      if (id >= V) continue;
+      atomicOr(&L.hbits[(id >> 5) & (kVBits - 1u)], 1u << (id & 31u));
+      uint32_t h = (id * 2654435761u) >> 21;
+      for (uint32_t probe = 0; probe < kVHash; ++probe) {
+        const uint32_t old = atomicCAS(&L.hkey[h], kHashEmpty, id);
+        if (old == id || old == kHashEmpty) {
+          if (old == kHashEmpty && atomicAdd(&L.misc[kVDistinct], 1u) >= kVMaxDistinct) L.misc[kVFail] = 1u;
+          atomicAdd(&L.D[h], 1u);
+          break;
+        }
+        h = (h + 1u) & (kVHash - 1u);
+      }
+    }
+    __syncthreads();
+    if (L.misc[kVFail]) return false;
+    for (uint32_t s = tid; s < kVHash; s += kBlock) {
+      const uint32_t id = L.hkey[s];
+      if (id != kHashEmpty) {
+        float v = row[id];
+        if (masked_out(a, id)) v = -INFINITY;
+        L.hval[s] = apply_penalty(v, L.D[s], rp);
+      }
+    }
+    __syncthreads();
+  }
+  auto wval = [&a, &L, use_pen, T](uint32_t i, float v) __attribute__((always_inline)) -> float {
+    if (masked_out(a, i)) v = -INFINITY;
+    if (use_pen && ((L.hbits[(i >> 5) & (kVBits - 1u)] >> (i & 31u)) & 1u)) {
+      uint32_t h = (i * 2654435761u) >> 21;
+      for (uint32_t probe = 0; probe < kVHash; ++probe) {
+        const uint32_t k = L.hkey[h];
+        if (k == i) {
+          v = L.hval[h];
+          break;
+        }
+        if (k == kHashEmpty) break;
+        h = (h + 1u) & (kVHash - 1u);
+      }
+    }
+    return v / T;  // generate.rs:357-359
+  };
+  const StreamSrc<decltype(wval)> src{row, V, vec4, wval};
+  return vocab_folds(a, b, len_b, P, L, src);
+}
+
+}  // namespace llmhip

@@ -77,7 +77,7 @@ def test_decode_loop_top_k_path(sampler):
 
 
 def test_decode_loop_full_vocab_path(sampler):
-    """top_k = 0 (the sorting path), with a strong penalty and a short window."""
+    """top_k = 0 (the bucketed exact-fold path), with a strong penalty and a short window."""
     _run(sampler, 2048, make_params(1.0, 0, 0.9, 0.02, 1.8), window=16, cap=16)
 
 

@@ -1,0 +1,127 @@
+"""GPU: the full-vocabulary kernel (top_k == 0 or top_k >= V) against the oracle.
+
+These calls ask for no probabilities, which is what routes full-vocabulary
+rows to the bucketed exact-fold kernel (a call that wants out_probs sorts
+them instead). The bar is strict: every id, kept count and RNG state equals
+the oracle's; no tie allowance is used.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from scriptonait_amd.workloads import PARAMS_DTYPE, make_params, make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+def _both(sampler, logits, params, seeds, hist=None, offs=None, V=None, allowed=None):
+    g = sampler.sample_host(logits, params, seeds, hist, offs, allowed=allowed, V=V, want_probs=False)
+    o = oracle.sample_batch(logits, params, seeds, hist, offs, allowed=allowed, V=V, threads=8)
+    return g, o
+
+
+def _assert_same(g, o, label):
+    bad = np.nonzero(g.ids != o.ids)[0]
+    assert bad.size == 0, f"{label}: ids differ at rows {bad[:8]} gpu={g.ids[bad[:8]]} oracle={o.ids[bad[:8]]}"
+    bad = np.nonzero(g.kept != o.kept)[0]
+    assert bad.size == 0, f"{label}: kept differs at rows {bad[:8]} gpu={g.kept[bad[:8]]} oracle={o.kept[bad[:8]]}"
+    assert np.array_equal(g.rng_state, o.rng_state), f"{label}: rng state differs"
+
+
+@pytest.mark.parametrize("cfg,B", [(4, 96), (5, 32)])
+def test_full_vocab_configs(sampler, cfg, B):
+    w = make_workload(cfg, B=B)
+    g, o = _both(sampler, w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
+    _assert_same(g, o, w.name)
+
+
+@pytest.mark.parametrize("cfg", [4, 5])
+def test_full_vocab_configs_other_seed(sampler, cfg):
+    w = make_workload(cfg, data_seed=11, B=24)
+    g, o = _both(sampler, w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
+    _assert_same(g, o, w.name)
+
+
+def _adversarial_rows(rs, B, V):
+    logits = np.zeros((B, V), dtype=np.float32)
+    prm = np.zeros(B, dtype=PARAMS_DTYPE)
+    for b in range(B):
+        kind = b % 8
+        if kind == 0:
+            l = rs.normal(0, 1, V)
+        elif kind == 1:
+            l = rs.normal(0, 5, V)
+        elif kind == 2:
+            l = np.round(rs.normal(0, 2, V) * 4) / 4  # many equal values
+        elif kind == 3:
+            l = np.zeros(V)  # all equal: every fold is over equal terms
+        elif kind == 4:
+            l = rs.normal(0, 0.01, V)  # flat
+        elif kind == 5:
+            l = rs.gumbel(0, 1, V)
+            l[rs.integers(0, V, V // 3)] = -np.inf
+        elif kind == 6:
+            l = rs.normal(0, 1, V)
+            l[rs.integers(0, V)] = 30.0  # one token takes all the mass
+        else:
+            l = rs.normal(0, 1, V) * 40.0  # mass spread over very few tokens
+        logits[b] = l.astype(np.float32)
+        T = [0.5, 0.9, 1.0, 1.7][b % 4]
+        tp = [1.0, 0.98, 0.9, 0.5, 0.1][(b // 4) % 5]
+        mp = [0.0, 0.0, 0.02, 0.3][(b // 3) % 4]
+        k = 0 if b % 5 else V  # top_k >= V keeps the whole vocabulary too
+        prm[b] = (T, k, tp, mp, 1.0)
+    return logits, prm
+
+
+@pytest.mark.parametrize("V", [5, 300, 4096, 9000, 50257])
+def test_adversarial_rows(sampler, V):
+    rs = np.random.default_rng(V)
+    B = 40
+    logits, prm = _adversarial_rows(rs, B, V)
+    seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
+    g, o = _both(sampler, logits, prm, seeds, V=V)
+    _assert_same(g, o, f"adversarial V={V}")
+
+
+@pytest.mark.parametrize("rp", [1.3, 0.7])
+def test_repetition_penalty_histories(sampler, rp):
+    rs = np.random.default_rng(7)
+    B, V, H = 24, 20000, 1500
+    logits = rs.normal(0, 2, (B, V)).astype(np.float32)
+    hist = rs.integers(0, V + 50, size=B * H).astype(np.uint32)  # some ids >= V are ignored
+    hist[::7] = hist[0]  # one id repeated many times
+    offs = (np.arange(B + 1) * H).astype(np.uint32)
+    prm = make_params(0.9, 0, 0.95, 0.02, rp)
+    seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
+    g, o = _both(sampler, logits, prm, seeds, hist, offs, V=V)
+    _assert_same(g, o, f"penalty {rp}")
+
+
+def test_rows_the_kernel_hands_to_the_sorting_path(sampler):
+    """NaN and +inf logits, an all -inf row and a history longer than the
+    LDS count table: these rows take the sorting path inside the kernel."""
+    rs = np.random.default_rng(5)
+    B, V = 6, 3000
+    logits = rs.normal(0, 1, (B, V)).astype(np.float32)
+    logits[0, 17] = np.nan
+    logits[1, 5] = np.inf
+    logits[2, :] = -np.inf
+    H = 5000
+    hist = rs.integers(0, V, size=B * H).astype(np.uint32)
+    offs = np.array([0, 0, 0, 0, H, 2 * H, 2 * H], dtype=np.uint32)
+    prm = make_params(1.0, 0, 0.9, 0.0, 1.2)
+    seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
+    g, o = _both(sampler, logits, prm, seeds, hist[: 2 * H], offs, V=V)
+    _assert_same(g, o, "handed-over rows")
+
+
+def test_allowed_mask_full_vocab(sampler):
+    rs = np.random.default_rng(9)
+    B, V = 16, 8192
+    logits = rs.normal(0, 2, (B, V)).astype(np.float32)
+    allowed = (rs.random(V - 500) < 0.3).astype(np.uint8)
+    prm = make_params(0.8, 0, 0.95, 0.05, 1.0)
+    seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
+    g, o = _both(sampler, logits, prm, seeds, V=V, allowed=allowed)
+    _assert_same(g, o, "allowed mask")
