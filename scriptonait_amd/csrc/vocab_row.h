@@ -50,6 +50,7 @@ constexpr uint32_t kVTies = 256;           // ties in certain buckets per fold
 constexpr uint32_t kVHash = 2048;          // repetition-count table slots
 constexpr uint32_t kVMaxDistinct = 1536;   // distinct history ids the table takes
 constexpr uint32_t kVBits = 4096;          // words of the history filter (bit id mod 2^17)
+constexpr uint32_t kVListCap = 65536;      // min-p candidates listed per row
 constexpr uint32_t kHashEmpty = 0xffffffffu;
 constexpr int32_t kNoE = -1000;            // segment without certain buckets
 constexpr uint32_t kNoPos = 0xffffffffu;
@@ -67,7 +68,8 @@ enum : uint32_t {
   kVStopBk = 6,
   kVF = 7,
   kVDistinct = 8,  // distinct history ids
-  kVMisc = 9,
+  kVCand = 9,      // min-p candidates listed
+  kVMisc = 10,
 };
 
 struct VocabLds {
@@ -211,6 +213,21 @@ struct StreamSrc {
         for (int s = 0; s < 8; ++s) f(wval(i + kBlock * s, v[s]), i + kBlock * s);
       }
       for (; i < V; i += kBlock) f(wval(i, row[i]), i);
+    }
+  }
+};
+
+// The min-p candidates of a row, listed by the histogram pass as (key, id)
+// pairs in the row's scratch: once S is known, the top-p and walk folds read
+// only these when every bucket that can pass min-p was listed.
+struct ListSrc {
+  const uint2* list;
+  uint32_t n;
+  template <class F>
+  __device__ __forceinline__ void for_each(F&& f) const {
+    for (uint32_t j = threadIdx.x; j < n; j += kBlock) {
+      const uint2 e = list[j];
+      f(key2f(e.x), e.y);
     }
   }
 };
@@ -664,11 +681,20 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   static_assert(sizeof(L.zkey) + sizeof(L.zid) >= kVB * sizeof(unsigned long long), "amass");
   unsigned long long* amass = reinterpret_cast<unsigned long long*>(L.zkey);
   for (uint32_t k = tid; k < kVB; k += kBlock) amass[k] = 0ull;
+  // With min-p on, elements of the buckets that can reach p >= min_p * p_0
+  // (x >= ~min_p, so y >= ~ln(min_p); two buckets of slack) are listed.
+  const uint32_t list_cap = (uint32_t)min((uint64_t)a.scratch_row_words / 2u, (uint64_t)kVListCap);
+  const uint32_t kc = P.min_p > 0.0f && P.min_p <= 1.0f ? (uint32_t)fminf(-logf(P.min_p) * kVR + 2.0f, (float)(kVB - 1u)) : 0u;
+  uint2* list = reinterpret_cast<uint2*>(a.scratch + (size_t)b * a.scratch_row_words);
   __syncthreads();
-  src.for_each([&](float w, uint32_t) __attribute__((always_inline)) {
+  src.for_each([&](float w, uint32_t i) __attribute__((always_inline)) {
     const float y = w - mx;
     const uint32_t k = vbucket(y);
     atomicAdd(&L.cnt[k], 1u);
+    if (k <= kc && kc) {
+      const uint32_t s = atomicAdd(&L.misc[kVCand], 1u);
+      if (s < list_cap) list[s] = make_uint2(f2key(w), i);
+    }
     const uint32_t xb = __float_as_uint(__expf(y));
     const int sh = (int)((xb >> 23) & 255u) - 127 + 17;  // x * 2^40 = m * 2^(e + 17)
     const unsigned long long m = (xb & 0x7fffffu) | 0x800000u;
@@ -687,43 +713,52 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   if (!(S > 0.0f) || !isfinite(S)) return false;
 
   // generate.rs:378-409: p = x / S; min-p by value (p is monotone along the
-  // order); the top-p cumulative, whose value at the cut is the total.
+  // order); the top-p cumulative, whose value at the cut is the total. Then
+  // generate.rs:411-419: r = u * total, and the walk.
   const float p0 = 1.0f / S;
   const float thr = P.min_p > 0.0f ? P.min_p * p0 : 0.0f;
-  fs = FoldSpec{0.0f, S, thr, P.top_p < 1.0f ? P.top_p : INFINITY, kVB, kVB, kNoPos, false};
-  if (!run_fold(fs, mx, L, src, r)) return false;
-  const bool cut = r.stop_pos != kNoPos;
-  uint32_t keep;
-  if (cut) {
-    keep = r.stop_pos + 1u;
-  } else if (P.min_p > 0.0f) {
-    keep = max(1u, L.misc[kVCount]);
-  } else {
-    keep = V;
+  auto cut_and_walk = [&](const auto& from) __attribute__((always_inline)) -> bool {
+    FoldSpec fc{0.0f, S, thr, P.top_p < 1.0f ? P.top_p : INFINITY, kVB, kVB, kNoPos, false};
+    FoldRes rc;
+    if (!run_fold(fc, mx, L, from, rc)) return false;
+    const bool cut = rc.stop_pos != kNoPos;
+    uint32_t keep;
+    if (cut) {
+      keep = rc.stop_pos + 1u;
+    } else if (P.min_p > 0.0f) {
+      keep = max(1u, L.misc[kVCount]);
+    } else {
+      keep = V;
+    }
+    uint64_t st = a.rng_state[b];
+    const float u = next_f32(st);
+    const float r0 = u * rc.F;
+    FoldSpec fw{r0, S, thr, INFINITY, cut ? rc.stop_bk + 1u : kVB, cut ? rc.stop_bk : kVB, keep, true};
+    FoldRes rw;
+    if (!run_fold(fw, mx, L, from, rw)) return false;
+    uint32_t pick;
+    if (rw.stop_pos != kNoPos) {
+      pick = rw.stop_id;
+    } else if (cut) {
+      pick = rc.stop_id;  // order[keep - 1]
+    } else {
+      return false;
+    }
+    if (tid == 0) {
+      store_result(a, b, pick, len_b);
+      a.rng_state[b] = st;
+      if (a.out_kept) a.out_kept[b] = keep;
+    }
+    return true;
+  };
+  // The list holds every element the two folds can include when the first
+  // bucket past it lies wholly below the min-p threshold.
+  const uint32_t ncand = L.misc[kVCand];
+  if (kc && ncand <= list_cap && kc + 1u < kVB &&
+      glibc_expf_tab(-(float)(kc + 1u) / kVR, L.exptab) / S < thr) {
+    return cut_and_walk(ListSrc{list, ncand});
   }
-  const float total = r.F;
-  const uint32_t cut_id = r.stop_id, cut_bk = r.stop_bk;
-
-  // generate.rs:411-419: r = u * total, then the walk.
-  uint64_t st = a.rng_state[b];
-  const float u = next_f32(st);
-  const float r0 = u * total;
-  fs = FoldSpec{r0, S, thr, INFINITY, cut ? cut_bk + 1u : kVB, cut ? cut_bk : kVB, keep, true};
-  if (!run_fold(fs, mx, L, src, r)) return false;
-  uint32_t pick;
-  if (r.stop_pos != kNoPos) {
-    pick = r.stop_id;
-  } else if (cut) {
-    pick = cut_id;  // order[keep - 1]
-  } else {
-    return false;
-  }
-  if (tid == 0) {
-    store_result(a, b, pick, len_b);
-    a.rng_state[b] = st;
-    if (a.out_kept) a.out_kept[b] = keep;
-  }
-  return true;
+  return cut_and_walk(src);
 }
 
 // Returns false (uniformly) when the row must go to general_row.
