@@ -90,10 +90,11 @@ struct VocabLds {
   unsigned long long seg[kVZones + 1];
   int32_t segE[kVZones + 1];
   uint32_t segTub[kVZones + 1];  // largest term bound of the segment (walk)
-  // Gathered zone elements and their sorted order. Before the first fold,
-  // zkey/zid hold the buckets' masses as 64-bit fixed point (amass).
-  alignas(8) uint32_t zkey[kVZoneEls];
-  uint32_t zid[kVZoneEls];
+  // Gathered zone elements, packed as key << 32 | ~id so that a larger value
+  // comes first in the reference's order; after the sort, term << 32 | ~id.
+  // zperm[base + r] is the element at sorted position r of its zone. Before
+  // the first fold, zpk holds the buckets' masses (amass).
+  unsigned long long zpk[kVZoneEls];
   uint16_t zperm[kVZoneEls];
   // Ties in certain buckets: key, id, ulp count, bucket; ulp sum above each.
   uint32_t tkey[kVTies], tidx[kVTies], tq[kVTies], tbk[kVTies], tab[kVTies];
@@ -400,8 +401,7 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
     if (c == kBZone) {
       const uint32_t z = L.zs[k];
       const uint32_t e = L.zbase[z] + atomicAdd(&L.zcur[z], 1u);
-      L.zkey[e] = f2key(w);
-      L.zid[e] = i;
+      L.zpk[e] = ((unsigned long long)f2key(w) << 32) | (uint32_t)~i;
     } else {
       bool tie, big;
       const uint32_t q = rne_units(t, L.segE[L.zs[k]], tie, big);
@@ -490,15 +490,26 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
   for (int j = 0; j < 4; ++j)
     if (cl[j] == kBCert) atomicAdd(&L.seg[L.zs[k0 + j]], (unsigned long long)L.D[k0 + j]);
 
-  // Sort each gathering zone by (key desc, id asc): rank by counting.
+  // Sort each gathering zone by (key desc, id asc), ranking by counting
+  // larger packed values; then replace each key by the element's term, so
+  // the replay reads terms.
   for (uint32_t z = wave; z < nz; z += kWaves) {
     if (L.cls[L.zb[z]] != kBZone) continue;
     const uint32_t base = L.zbase[z], n = L.zcur[z];
+    const unsigned long long* pk = L.zpk + base;
     for (uint32_t i = lane; i < n; i += 64u) {
-      const uint32_t ki = L.zkey[base + i], ii = L.zid[base + i];
+      const unsigned long long me = pk[i];
       uint32_t r = 0;
-      for (uint32_t j = 0; j < n; ++j) r += before(L.zkey[base + j], L.zid[base + j], ki, ii) ? 1u : 0u;
+      uint32_t j = 0;
+      for (; j + 4u <= n; j += 4u)
+        r += (pk[j] > me ? 1u : 0u) + (pk[j + 1] > me ? 1u : 0u) + (pk[j + 2] > me ? 1u : 0u) + (pk[j + 3] > me ? 1u : 0u);
+      for (; j < n; ++j) r += pk[j] > me ? 1u : 0u;
       L.zperm[base + r] = (uint16_t)i;
+    }
+    for (uint32_t i = lane; i < n; i += 64u) {
+      const unsigned long long v = L.zpk[base + i];
+      const float t = term_of(glibc_expf_tab(key2f((uint32_t)(v >> 32)) - mx, L.exptab));
+      L.zpk[base + i] = ((unsigned long long)__float_as_uint(t) << 32) | (uint32_t)v;
     }
   }
   __syncthreads();
@@ -568,10 +579,10 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
         const uint32_t r = r0 + lane;
         float t = 0.0f;
         uint32_t id = 0u;
-        if (r < n) {  // the term again, as the exact pass made it
-          const uint32_t e = base + L.zperm[base + r];
-          t = term_of(glibc_expf_tab(key2f(L.zkey[e]) - mx, L.exptab));
-          id = L.zid[e];
+        if (r < n) {
+          const unsigned long long v = L.zpk[base + L.zperm[base + r]];
+          t = __uint_as_float((uint32_t)(v >> 32));
+          id = ~(uint32_t)v;
         }
         const bool live = r < n;
         const bool past = live && p0 + r >= fs.pos_end;
@@ -678,8 +689,8 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
 
   // Bucket counts and approximate masses. The masses add up as integers
   // (x in units of 2^-40): LDS integer atomics are much faster than float ones.
-  static_assert(sizeof(L.zkey) + sizeof(L.zid) >= kVB * sizeof(unsigned long long), "amass");
-  unsigned long long* amass = reinterpret_cast<unsigned long long*>(L.zkey);
+  static_assert(sizeof(L.zpk) >= kVB * sizeof(unsigned long long), "amass");
+  unsigned long long* amass = L.zpk;
   for (uint32_t k = tid; k < kVB; k += kBlock) amass[k] = 0ull;
   // With min-p on, elements of the buckets that can reach p >= min_p * p_0
   // (x >= ~min_p, so y >= ~ln(min_p); two buckets of slack) are listed.
