@@ -546,97 +546,123 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
       F = F + tv;
       return F >= fs.stop_ge;
     };
-    for (uint32_t z = 0; z <= nz && !fail && !stopped; ++z) {
-      const int Es = L.segE[z];
-      if (Es != kNoE) {
-        if (!apply_units(Es, L.seg[z])) fail = true;
-        else if (!fs.sub && F >= fs.stop_ge) fail = true;
-        else if (fs.sub && F < __uint_as_float(L.segTub[z])) fail = true;
+    for (uint32_t zc = 0; zc <= nz && !fail && !stopped; zc += 64u) {
+      // Segment and zone data of zones zc .. zc + 63, one zone per lane, so
+      // the walk through them reads registers.
+      const uint32_t zl = zc + lane;
+      uint32_t mSegE = (uint32_t)kNoE, mSegTub = 0u, mK = 0u, mBase = 0u, mN = 0u, mP0 = 0u, mCls = 0u;
+      uint32_t mE = 0u, mTub = 0u, mT0 = 0u, mTn = 0u, mD = 0u;
+      uint64_t mSeg = 0ull;
+      if (zl <= nz) {
+        mSegE = (uint32_t)L.segE[zl];
+        mSeg = L.seg[zl];
+        mSegTub = L.segTub[zl];
       }
-      if (z == nz || fail) break;
-      const uint32_t k = L.zb[z];
-      if (L.cls[k] == kBTie) {
-        const int E = L.zE[z];
-        uint32_t prev = 0;
-        const uint32_t t0 = L.zt0[z], tn = L.ztn[z];
-        for (uint32_t u = 0; u < tn && !fail; ++u) {
-          const uint32_t s = L.tord[t0 + u];
-          const uint32_t ab = L.tab[s];
-          if (!apply_units(E, ab - prev)) fail = true;
-          prev = ab;
-          const uint32_t q = L.tq[s];
-          const uint32_t par = (__float_as_uint(F) ^ q) & 1u;  // parity of M - q or M + q
-          if (!fail && !apply_units(E, (uint64_t)q + par)) fail = true;
-        }
-        if (!fail && !apply_units(E, L.D[k] - prev)) fail = true;
-        if (!fail && !fs.sub && F >= fs.stop_ge) fail = true;
-        if (!fail && fs.sub && F < __uint_as_float(L.zTub[z])) fail = true;
-        continue;
+      if (zl < nz) {
+        mK = L.zb[zl];
+        mBase = L.zbase[zl];
+        mN = L.zcur[zl];
+        mP0 = L.zpos[zl];
+        mCls = L.cls[mK];
+        mE = (uint32_t)L.zE[zl];
+        mTub = L.zTub[zl];
+        mT0 = L.zt0[zl];
+        mTn = L.ztn[zl];
+        mD = L.D[mK];
       }
-      const uint32_t base = L.zbase[z], n = L.zcur[z], p0 = L.zpos[z];
-      uint32_t r0 = 0;
-      while (r0 < n && !stopped) {
-        const uint32_t r = r0 + lane;
-        float t = 0.0f;
-        uint32_t id = 0u;
-        if (r < n) {
-          const unsigned long long v = L.zpk[base + L.zperm[base + r]];
-          t = __uint_as_float((uint32_t)(v >> 32));
-          id = ~(uint32_t)v;
+      for (uint32_t zi = 0; zi < 64u && zc + zi <= nz && !fail && !stopped; ++zi) {
+        const uint32_t z = zc + zi;
+        const int Es = (int)readlane_u32(mSegE, zi);
+        if (Es != kNoE) {
+          if (!apply_units(Es, readlane_u64(mSeg, zi))) fail = true;
+          else if (!fs.sub && F >= fs.stop_ge) fail = true;
+          else if (fs.sub && F < __uint_as_float(readlane_u32(mSegTub, zi))) fail = true;
         }
-        const bool live = r < n;
-        const bool past = live && p0 + r >= fs.pos_end;
-        const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
-        uint32_t ev_lane = 0u;  // first lane stepped in f32
-        uint32_t done = 0u;     // lanes before it, folded as integers
-        if (F > 0.0f && ef >= 1u && ef <= 254u) {
-          const int E = (int)ef - 127;
-          const uint32_t M = (fb & 0x7fffffu) | 0x800000u;
-          bool tie = false, big = false;
-          const uint32_t q = live && !past ? rne_units(t, E, tie, big) : 0u;
-          const uint32_t incl = wave_incl_scan(q), excl = incl - q;
-          bool ev;
-          if (!fs.sub) {
-            const uint64_t Mi = (uint64_t)M + incl;
-            ev = tie || big || Mi >= (1ull << 24) || from_units((uint32_t)Mi, E) >= fs.stop_ge;
-          } else {
-            const bool ub = (uint64_t)excl + (1ull << 23) + 1ull > M;
-            const bool ui = (uint64_t)incl + (1ull << 23) + 1ull > M;
-            ev = tie || big || ub || ui || from_units(M - excl, E) < t;
+        if (z == nz || fail) break;
+        const uint32_t k = readlane_u32(mK, zi);
+        if (readlane_u32(mCls, zi) == kBTie) {
+          const int E = (int)readlane_u32(mE, zi);
+          uint32_t prev = 0;
+          const uint32_t t0 = readlane_u32(mT0, zi), tn = readlane_u32(mTn, zi);
+          for (uint32_t u = 0; u < tn && !fail; ++u) {
+            const uint32_t s = L.tord[t0 + u];
+            const uint32_t ab = L.tab[s];
+            if (!apply_units(E, ab - prev)) fail = true;
+            prev = ab;
+            const uint32_t q = L.tq[s];
+            const uint32_t par = (__float_as_uint(F) ^ q) & 1u;  // parity of M - q or M + q
+            if (!fail && !apply_units(E, (uint64_t)q + par)) fail = true;
           }
-          ev = live && (ev || past);
-          const uint64_t m = __ballot(ev);
-          ev_lane = m ? (uint32_t)__ffsll((unsigned long long)m) - 1u : 64u;
-          done = min(ev_lane, n - r0);
-          if (done) {
-            const uint32_t sum = readlane_u32(incl, done - 1u);
-            const uint64_t M2 = fs.sub ? (uint64_t)M - sum : (uint64_t)M + sum;
-            F = from_units((uint32_t)M2, E);
-          }
-        }
-        if (r0 + done >= n) {
-          r0 = n;
-          break;
-        }
-        if (done == 64u) {  // no event in these 64
-          r0 += 64u;
+          if (!fail && !apply_units(E, readlane_u32(mD, zi) - prev)) fail = true;
+          if (!fail && !fs.sub && F >= fs.stop_ge) fail = true;
+          if (!fail && fs.sub && F < __uint_as_float(readlane_u32(mTub, zi))) fail = true;
           continue;
         }
-        // Element ev_lane (or the first one when F is not a normal number).
-        const uint32_t le = done;
-        const uint32_t pos = p0 + r0 + le;
-        if (pos >= fs.pos_end) {
-          stopped = true;  // the rest of the fold is outside it
-          break;
+        const uint32_t base = readlane_u32(mBase, zi), n = readlane_u32(mN, zi), p0 = readlane_u32(mP0, zi);
+        uint32_t r0 = 0;
+        while (r0 < n && !stopped) {
+          const uint32_t r = r0 + lane;
+          float t = 0.0f;
+          uint32_t id = 0u;
+          if (r < n) {
+            const unsigned long long v = L.zpk[base + L.zperm[base + r]];
+            t = __uint_as_float((uint32_t)(v >> 32));
+            id = ~(uint32_t)v;
+          }
+          const bool live = r < n;
+          const bool past = live && p0 + r >= fs.pos_end;
+          const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
+          uint32_t ev_lane = 0u;  // first lane stepped in f32
+          uint32_t done = 0u;     // lanes before it, folded as integers
+          if (F > 0.0f && ef >= 1u && ef <= 254u) {
+            const int E = (int)ef - 127;
+            const uint32_t M = (fb & 0x7fffffu) | 0x800000u;
+            bool tie = false, big = false;
+            const uint32_t q = live && !past ? rne_units(t, E, tie, big) : 0u;
+            const uint32_t incl = wave_incl_scan(q), excl = incl - q;
+            bool ev;
+            if (!fs.sub) {
+              const uint64_t Mi = (uint64_t)M + incl;
+              ev = tie || big || Mi >= (1ull << 24) || from_units((uint32_t)Mi, E) >= fs.stop_ge;
+            } else {
+              const bool ub = (uint64_t)excl + (1ull << 23) + 1ull > M;
+              const bool ui = (uint64_t)incl + (1ull << 23) + 1ull > M;
+              ev = tie || big || ub || ui || from_units(M - excl, E) < t;
+            }
+            ev = live && (ev || past);
+            const uint64_t m = __ballot(ev);
+            ev_lane = m ? (uint32_t)__ffsll((unsigned long long)m) - 1u : 64u;
+            done = min(ev_lane, n - r0);
+            if (done) {
+              const uint32_t sum = readlane_u32(incl, done - 1u);
+              const uint64_t M2 = fs.sub ? (uint64_t)M - sum : (uint64_t)M + sum;
+              F = from_units((uint32_t)M2, E);
+            }
+          }
+          if (r0 + done >= n) {
+            r0 = n;
+            break;
+          }
+          if (done == 64u) {  // no event in these 64
+            r0 += 64u;
+            continue;
+          }
+          // Element ev_lane (or the first one when F is not a normal number).
+          const uint32_t le = done;
+          const uint32_t pos = p0 + r0 + le;
+          if (pos >= fs.pos_end) {
+            stopped = true;  // the rest of the fold is outside it
+            break;
+          }
+          if (step(readlane_f32(t, le))) {
+            stop_pos = pos;
+            stop_id = readlane_u32(id, le);
+            stop_bk = k;
+            stopped = true;
+            break;
+          }
+          r0 += le + 1u;
         }
-        if (step(readlane_f32(t, le))) {
-          stop_pos = pos;
-          stop_id = readlane_u32(id, le);
-          stop_bk = k;
-          stopped = true;
-          break;
-        }
-        r0 += le + 1u;
       }
     }
     // Past the end without a stop, although a bucket was certain to lie
