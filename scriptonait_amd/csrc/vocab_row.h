@@ -69,15 +69,17 @@ enum : uint32_t {
   kVF = 7,
   kVDistinct = 8,  // distinct history ids
   kVCand = 9,      // min-p candidates listed
-  kVMisc = 10,
+  kVSplitDone = 10,  // waves done with the tie split
+  kVMisc = 11,
 };
 
 struct VocabLds {
   uint32_t cnt[kVB];   // elements per bucket
   float asum[kVB];     // approximate sum of x per bucket
   uint32_t D[kVB];     // exact ulp counts of a fold's certain buckets
-  uint16_t zs[kVB];    // zone slot (zones) or segment index (certain buckets)
-  uint8_t cls[kVB];
+  // Per bucket, one word: class << 24 | (binade + 128) << 16 | slot, the slot
+  // being the zone slot (zones) or the segment index (certain buckets).
+  uint32_t binfo[kVB];
   // Zones in bucket order; segment z holds the certain buckets before zone z.
   uint32_t zb[kVZones];
   uint32_t zbase[kVZones + 1];
@@ -108,6 +110,10 @@ struct VocabLds {
   uint32_t misc[kVMisc];
   uint64_t exptab[32];
 };
+
+__device__ __forceinline__ uint32_t bcls(uint32_t bi) { return bi >> 24; }
+__device__ __forceinline__ uint32_t bslot(uint32_t bi) { return bi & 0xffffu; }
+__device__ __forceinline__ int bbinade(uint32_t bi) { return (int)((bi >> 16) & 255u) - 128; }
 
 __device__ __forceinline__ uint32_t vbucket(float y) {
   const float ny = -y;
@@ -176,26 +182,29 @@ struct StreamSrc {
   uint32_t V;
   bool vec4;
   WV wval;
+  // Threads t0 .. t0 + nt - 1 visit the row between them (the caller's
+  // thread is one of them).
   template <class F>
-  __device__ __forceinline__ void for_each(F&& f) const {
+  __device__ __forceinline__ void for_each_part(F&& f, uint32_t t0, uint32_t nt) const {
+    const uint32_t t = threadIdx.x - t0;
     if (vec4) {
       const float4* r4 = reinterpret_cast<const float4*>(row);
       const uint32_t nq = (V + 3u) / 4u;
       float4 cur[4], nxt[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint32_t q = threadIdx.x + kBlock * s;
+        const uint32_t q = t + nt * s;
         cur[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      for (uint32_t q0 = 0; q0 < nq; q0 += 4u * kBlock) {
+      for (uint32_t q0 = 0; q0 < nq; q0 += 4u * nt) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const uint32_t q = q0 + 4u * kBlock + threadIdx.x + kBlock * s;
+          const uint32_t q = q0 + 4u * nt + t + nt * s;
           nxt[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const uint32_t i = 4u * (q0 + threadIdx.x + kBlock * s);
+          const uint32_t i = 4u * (q0 + t + nt * s);
           const float v[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
 #pragma unroll
           for (int c = 0; c < 4; ++c)
@@ -205,16 +214,20 @@ struct StreamSrc {
         for (int s = 0; s < 4; ++s) cur[s] = nxt[s];
       }
     } else {
-      uint32_t i = threadIdx.x;
-      for (; i + 7u * kBlock < V; i += 8u * kBlock) {
+      uint32_t i = t;
+      for (; i + 7u * nt < V; i += 8u * nt) {
         float v[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) v[s] = row[i + kBlock * s];
+        for (int s = 0; s < 8; ++s) v[s] = row[i + nt * s];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) f(wval(i + kBlock * s, v[s]), i + kBlock * s);
+        for (int s = 0; s < 8; ++s) f(wval(i + nt * s, v[s]), i + nt * s);
       }
-      for (; i < V; i += kBlock) f(wval(i, row[i]), i);
+      for (; i < V; i += nt) f(wval(i, row[i]), i);
     }
+  }
+  template <class F>
+  __device__ __forceinline__ void for_each(F&& f) const {
+    for_each_part(f, 0u, kBlock);
   }
 };
 
@@ -225,13 +238,31 @@ struct ListSrc {
   const uint2* list;
   uint32_t n;
   template <class F>
-  __device__ __forceinline__ void for_each(F&& f) const {
-    for (uint32_t j = threadIdx.x; j < n; j += kBlock) {
+  __device__ __forceinline__ void for_each_part(F&& f, uint32_t t0, uint32_t nt) const {
+    for (uint32_t j = threadIdx.x - t0; j < n; j += nt) {
       const uint2 e = list[j];
       f(key2f(e.x), e.y);
     }
   }
+  template <class F>
+  __device__ __forceinline__ void for_each(F&& f) const {
+    for_each_part(f, 0u, kBlock);
+  }
 };
+
+// exp(y) for -80 <= y <= 0 from the hardware exp2: y * log2(e) = k + f with
+// the product split exactly by an FMA, |f| <= 1/2, and v_exp_f32, whose
+// relative error on [-1/2, 1/2] is at most 1.4 * 2^-24 (measured over every
+// input). The result is within 2^-22 of glibc's expf (which is itself within
+// 0.502 ulp of exp). Used only to settle decisions that have that much room.
+__device__ __forceinline__ float cheap_x(float y) {
+  const float L1 = 0x1.715476p+0f, L2 = 0x1.4ae0bep-26f;  // log2(e) = L1 + L2 + O(2^-50)
+  const float hi = y * L1;
+  const float lo = __builtin_fmaf(y, L1, -hi) + y * L2;
+  const float kf = rintf(hi);
+  const float f = (hi - kf) + lo;  // hi - kf is exact
+  return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(f), (int)kf);
+}
 
 // One fold over the row's terms in sorted order (see the file comment).
 struct FoldSpec {
@@ -258,7 +289,8 @@ __device__ __forceinline__ bool before(uint32_t ka, uint32_t ia, uint32_t kb, ui
 }
 
 template <class Src>
-__device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds& L, const Src& src, FoldRes& res) {
+__device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds& L, const Src& src, FoldRes& res,
+                                         uint32_t* status) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t k0 = tid * 4u;
   const double scale = fs.S > 0.0f ? 1.0 / (double)fs.S : 1.0;
@@ -273,6 +305,7 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
     L.misc[kVBeyond] = kVB;
     L.misc[kVNTies] = 0u;
     L.misc[kVCount] = 0u;
+    L.misc[kVSplitDone] = 0u;
   }
 
   // Classification of this thread's 4 buckets from the approximate prefix.
@@ -363,7 +396,7 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
     for (int j = 0; j < 4; ++j) {
       const uint32_t k = k0 + j;
       if (cl[j] == kBZone || cl[j] == kBTie) {
-        L.zs[k] = (uint16_t)zi;
+        L.binfo[k] = ((uint32_t)cl[j] << 24) | ((uint32_t)(e4[j] + 128) << 16) | zi;
         L.zb[zi] = k;
         L.zbase[zi] = ei;
         L.zcur[zi] = again && cl[j] == kBZone ? L.D[k] : 0u;
@@ -373,11 +406,11 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
         ++zi;
         if (cl[j] == kBZone) ei += c4[j];
       } else if (cl[j] == kBCert) {
-        L.zs[k] = (uint16_t)zi;
+        L.binfo[k] = ((uint32_t)cl[j] << 24) | ((uint32_t)(e4[j] + 128) << 16) | zi;
         L.segE[zi] = e4[j];
         atomicMax(&L.segTub[zi], __float_as_uint(tub4[j]));
       }
-      L.cls[k] = cl[j];
+      if (cl[j] == kBSkip) L.binfo[k] = 0u;
       pos += c4[j];
     }
     if (tid == 0) L.zbase[nz] = nel;
@@ -389,35 +422,67 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
   __syncthreads();
 
   // Exact pass: certain buckets add ulp counts, zones gather, ties are listed.
+  // A term is first taken from a cheap exp (cheap_x: within 2^-22 of glibc's
+  // expf, and after the reciprocal multiply within 2^-20 of the exact term);
+  // the exact term is computed only when the cheap one cannot settle the
+  // min-p test or the ulp count (a scaled value within value * 2^-20 of a
+  // half-integer, or a term near the binade).
+  const float rcpS = fs.S > 0.0f ? 1.0f / fs.S : 1.0f;
   uint32_t nin = 0;
   src.for_each([&](float w, uint32_t i) __attribute__((always_inline)) {
     const float y = w - mx;
     const uint32_t k = vbucket(y);
-    const uint8_t c = L.cls[k];
+    const uint32_t bi = L.binfo[k];
+    const uint32_t c = bcls(bi);
     if (c == kBSkip) return;
-    const float t = term_of(glibc_expf_tab(y, L.exptab));
-    if (fs.thr > 0.0f && !(t >= fs.thr)) return;
+    const bool cheap = y >= -80.0f;
+    const float ta = cheap ? cheap_x(y) * rcpS : 0.0f;
+    float t = -1.0f;  // the exact term, once computed
+    if (fs.thr > 0.0f) {
+      bool in;
+      if (cheap && ta >= fs.thr * (1.0f + 0x1p-19f)) {
+        in = true;
+      } else if (cheap && ta < fs.thr * (1.0f - 0x1p-19f)) {
+        in = false;
+      } else {
+        t = term_of(glibc_expf_tab(y, L.exptab));
+        in = t >= fs.thr;
+      }
+      if (!in) return;
+    }
     ++nin;
     if (c == kBZone) {
-      const uint32_t z = L.zs[k];
+      const uint32_t z = bslot(bi);
       const uint32_t e = L.zbase[z] + atomicAdd(&L.zcur[z], 1u);
       L.zpk[e] = ((unsigned long long)f2key(w) << 32) | (uint32_t)~i;
-    } else {
-      bool tie, big;
-      const uint32_t q = rne_units(t, L.segE[L.zs[k]], tie, big);
-      if (big) L.misc[kVFail] = 1u;
-      if (tie) {
-        const uint32_t s = atomicAdd(&L.misc[kVNTies], 1u);
-        if (s < kVTies) {
-          L.tkey[s] = f2key(w);
-          L.tidx[s] = i;
-          L.tq[s] = q;
-          L.tbk[s] = k;
-          L.tab[s] = 0u;
+      return;
+    }
+    const int E = bbinade(bi);
+    if (cheap && t < 0.0f) {
+      const float v = __builtin_amdgcn_ldexpf(ta, 23 - E);  // ta in units of 2^(E-23), exactly
+      if (v < 0x1p22f) {
+        const float fl = floorf(v), fr = v - fl;
+        if (fabsf(fr - 0.5f) > v * 0x1p-20f + 0x1p-40f) {
+          atomicAdd(&L.D[k], (uint32_t)fl + (fr > 0.5f ? 1u : 0u));
+          return;
         }
-      } else {
-        atomicAdd(&L.D[k], q);
       }
+    }
+    if (t < 0.0f) t = term_of(glibc_expf_tab(y, L.exptab));
+    bool tie, big;
+    const uint32_t q = rne_units(t, E, tie, big);
+    if (big) L.misc[kVFail] = 1u;
+    if (tie) {
+      const uint32_t s = atomicAdd(&L.misc[kVNTies], 1u);
+      if (s < kVTies) {
+        L.tkey[s] = f2key(w);
+        L.tidx[s] = i;
+        L.tq[s] = q;
+        L.tbk[s] = k;
+        L.tab[s] = 0u;
+      }
+    } else {
+      atomicAdd(&L.D[k], q);
     }
   });
   nin = wave_sum(nin);
@@ -439,9 +504,12 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
       }
       L.tord[r] = (uint16_t)s;
     }
-    for (uint32_t s = tid; s < nt; s += kBlock) L.cls[L.tbk[s]] = kBTie;
+    for (uint32_t s = tid; s < nt; s += kBlock) {
+      const uint32_t k = L.tbk[s];  // every tie of a bucket writes the same word
+      L.binfo[k] = (L.binfo[k] & 0x00ffffffu) | ((uint32_t)kBTie << 24);
+    }
     for (uint32_t z = tid; z < nz; z += kBlock)
-      if (L.cls[L.zb[z]] == kBZone) L.D[L.zb[z]] = L.zcur[z];
+      if (bcls(L.binfo[L.zb[z]]) == kBZone) L.D[L.zb[z]] = L.zcur[z];
     for (uint32_t s = tid; s <= kVZones; s += kBlock) {
       L.segE[s] = kNoE;
       L.segTub[s] = 0u;
@@ -449,12 +517,12 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (L.cls[k0 + j] == kBTie) cl[j] = kBTie;
+      if (bcls(L.binfo[k0 + j]) == kBTie) cl[j] = kBTie;
     if (!layout(true)) return false;
     __syncthreads();
     for (uint32_t z = tid; z < nz; z += kBlock) {
       const uint32_t k = L.zb[z];
-      if (L.cls[k] != kBTie) continue;
+      if (bcls(L.binfo[k]) != kBTie) continue;
       uint32_t lo = 0, hi = nt;  // the bucket's ties are a run of tord
       while (lo < hi) {
         const uint32_t mid = (lo + hi) >> 1;
@@ -466,35 +534,17 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
       L.ztn[z] = (uint16_t)(e - lo);
     }
     __syncthreads();
-    src.for_each([&](float w, uint32_t i) __attribute__((always_inline)) {
-      const float y = w - mx;
-      const uint32_t k = vbucket(y);
-      if (L.cls[k] != kBTie) return;
-      const float t = term_of(glibc_expf_tab(y, L.exptab));
-      if (fs.thr > 0.0f && !(t >= fs.thr)) return;
-      const uint32_t z = L.zs[k];
-      bool tie, big;
-      const uint32_t q = rne_units(t, L.zE[z], tie, big);
-      if (tie || q == 0u) return;
-      const uint32_t key = f2key(w);
-      const uint32_t t0 = L.zt0[z], tn = L.ztn[z];
-      for (uint32_t u = 0; u < tn; ++u) {
-        const uint32_t s = L.tord[t0 + u];
-        if (before(key, i, L.tkey[s], L.tidx[s])) atomicAdd(&L.tab[s], q);
-      }
-    });
-    __syncthreads();
   }
 
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (cl[j] == kBCert) atomicAdd(&L.seg[L.zs[k0 + j]], (unsigned long long)L.D[k0 + j]);
+    if (cl[j] == kBCert) atomicAdd(&L.seg[bslot(L.binfo[k0 + j])], (unsigned long long)L.D[k0 + j]);
 
   // Sort each gathering zone by (key desc, id asc), ranking by counting
   // larger packed values; then replace each key by the element's term, so
   // the replay reads terms.
   for (uint32_t z = wave; z < nz; z += kWaves) {
-    if (L.cls[L.zb[z]] != kBZone) continue;
+    if (bcls(L.binfo[L.zb[z]]) != kBZone) continue;
     const uint32_t base = L.zbase[z], n = L.zcur[z];
     const unsigned long long* pk = L.zpk + base;
     for (uint32_t i = lane; i < n; i += 64u) {
@@ -514,9 +564,36 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
   }
   __syncthreads();
 
+  // Waves 1 .. 15 sum each tie bucket's ulp counts above each of its ties
+  // (a stream of the row) while wave 0 replays; wave 0 waits for them only
+  // when it reaches the first tie zone.
+  if (wave != 0 && nt) {
+    src.for_each_part([&](float w, uint32_t i) __attribute__((always_inline)) {
+      const float y = w - mx;
+      const uint32_t k = vbucket(y);
+      const uint32_t bi = L.binfo[k];
+      if (bcls(bi) != kBTie) return;
+      const float t = term_of(glibc_expf_tab(y, L.exptab));
+      if (fs.thr > 0.0f && !(t >= fs.thr)) return;
+      const uint32_t z = bslot(bi);
+      bool tie, big;
+      const uint32_t q = rne_units(t, bbinade(bi), tie, big);
+      if (tie || q == 0u) return;
+      const uint32_t key = f2key(w);
+      const uint32_t t0 = L.zt0[z], tn = L.ztn[z];
+      for (uint32_t u = 0; u < tn; ++u) {
+        const uint32_t s = L.tord[t0 + u];
+        if (before(key, i, L.tkey[s], L.tidx[s])) atomicAdd(&L.tab[s], q);
+      }
+    }, 64u, kBlock - 64u);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    if (lane == 0) atomicAdd(&L.misc[kVSplitDone], 1u);
+  }
+
   // Replay (wave 0): certain segments as integers, tie zones split at their
   // ties, gathering zones 64 elements at a time.
   if (wave == 0) {
+    bool split_ready = nt == 0u;
     float F = fs.F0;
     bool fail = false, stopped = false;
     uint32_t stop_pos = kNoPos, stop_id = 0, stop_bk = 0;
@@ -563,7 +640,7 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
         mBase = L.zbase[zl];
         mN = L.zcur[zl];
         mP0 = L.zpos[zl];
-        mCls = L.cls[mK];
+        mCls = bcls(L.binfo[mK]);
         mE = (uint32_t)L.zE[zl];
         mTub = L.zTub[zl];
         mT0 = L.zt0[zl];
@@ -581,6 +658,10 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
         if (z == nz || fail) break;
         const uint32_t k = readlane_u32(mK, zi);
         if (readlane_u32(mCls, zi) == kBTie) {
+          if (!split_ready) {
+            lds_wait(&L.misc[kVSplitDone], kWaves - 1u, status);
+            split_ready = true;
+          }
           const int E = (int)readlane_u32(mE, zi);
           uint32_t prev = 0;
           const uint32_t t0 = readlane_u32(mT0, zi), tn = readlane_u32(mTn, zi);
@@ -745,7 +826,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   // generate.rs:372-377: the softmax sum. The max element has x = 1, so S >= 1.
   FoldRes r;
   FoldSpec fs{0.0f, 0.0f, 0.0f, INFINITY, kVB, kVB, kNoPos, false};
-  if (!run_fold(fs, mx, L, src, r)) return false;
+  if (!run_fold(fs, mx, L, src, r, a.status)) return false;
   const float S = r.F;
   if (!(S > 0.0f) || !isfinite(S)) return false;
 
@@ -757,7 +838,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   auto cut_and_walk = [&](const auto& from) __attribute__((always_inline)) -> bool {
     FoldSpec fc{0.0f, S, thr, P.top_p < 1.0f ? P.top_p : INFINITY, kVB, kVB, kNoPos, false};
     FoldRes rc;
-    if (!run_fold(fc, mx, L, from, rc)) return false;
+    if (!run_fold(fc, mx, L, from, rc, a.status)) return false;
     const bool cut = rc.stop_pos != kNoPos;
     uint32_t keep;
     if (cut) {
@@ -772,7 +853,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
     const float r0 = u * rc.F;
     FoldSpec fw{r0, S, thr, INFINITY, cut ? rc.stop_bk + 1u : kVB, cut ? rc.stop_bk : kVB, keep, true};
     FoldRes rw;
-    if (!run_fold(fw, mx, L, from, rw)) return false;
+    if (!run_fold(fw, mx, L, from, rw, a.status)) return false;
     uint32_t pick;
     if (rw.stop_pos != kNoPos) {
       pick = rw.stop_id;
@@ -878,7 +959,7 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
         h = (h + 1u) & (kVHash - 1u);
       }
     }
-    return v / T;  // generate.rs:357-359
+    return T == 1.0f ? v : v / T;  // generate.rs:357-359 (w / 1 is w)
   };
   const StreamSrc<decltype(wval)> src{row, V, vec4, wval};
   return vocab_folds(a, b, len_b, P, L, src);
