@@ -74,7 +74,7 @@ def _adversarial_rows(rs, B, V):
     return logits, prm
 
 
-@pytest.mark.parametrize("V", [5, 300, 4096, 9000, 50257])
+@pytest.mark.parametrize("V", [1, 2, 5, 300, 4096, 9000, 50257])
 def test_adversarial_rows(sampler, V):
     rs = np.random.default_rng(V)
     B = 40
@@ -125,3 +125,16 @@ def test_allowed_mask_full_vocab(sampler):
     seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
     g, o = _both(sampler, logits, prm, seeds, V=V, allowed=allowed)
     _assert_same(g, o, "allowed mask")
+
+
+@pytest.mark.parametrize("V,ld", [(1001, 1003), (8191, 8193), (40000, 40001)])
+def test_rows_with_an_odd_stride(sampler, V, ld):
+    """ld % 4 != 0 (and odd V): the kernel reads the row with dword loads."""
+    rs = np.random.default_rng(V)
+    B = 12
+    logits = np.full((B, ld), 1e30, dtype=np.float32)  # padding past V must never be read as logits
+    logits[:, :V] = rs.normal(0, 2, (B, V)).astype(np.float32)
+    prm = make_params(0.9, 0, 0.95, 0.0, 1.0)
+    seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
+    g, o = _both(sampler, logits, prm, seeds, V=V)
+    _assert_same(g, o, f"odd stride V={V} ld={ld}")
