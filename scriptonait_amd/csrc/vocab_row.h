@@ -945,21 +945,32 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
     }
     __syncthreads();
   }
-  auto wval = [&a, &L, use_pen, T](uint32_t i, float v) __attribute__((always_inline)) -> float {
-    if (masked_out(a, i)) v = -INFINITY;
-    if (use_pen && ((L.hbits[(i >> 5) & (kVBits - 1u)] >> (i & 31u)) & 1u)) {
-      uint32_t h = (i * 2654435761u) >> 21;
-      for (uint32_t probe = 0; probe < kVHash; ++probe) {
-        const uint32_t k = L.hkey[h];
-        if (k == i) {
-          v = L.hval[h];
-          break;
+  // Each test on a row-wide condition is a branch of its own, so rows with
+  // no mask, no penalty or T == 1 pay nothing per element for it.
+  const uint8_t* allowed = a.allowed;
+  const uint32_t allowed_len = a.allowed_len, eos = a.eos_id;
+  const bool div_t = T != 1.0f;
+  auto wval = [allowed, allowed_len, eos, &L, use_pen, div_t, T](uint32_t i, float v)
+      __attribute__((always_inline)) -> float {
+    if (allowed) {  // generate.rs:333-341
+      if (i < allowed_len && i != eos && allowed[i] == 0) v = -INFINITY;
+    }
+    if (use_pen) {
+      if ((L.hbits[(i >> 5) & (kVBits - 1u)] >> (i & 31u)) & 1u) {
+        uint32_t h = (i * 2654435761u) >> 21;
+        for (uint32_t probe = 0; probe < kVHash; ++probe) {
+          const uint32_t k = L.hkey[h];
+          if (k == i) {
+            v = L.hval[h];
+            break;
+          }
+          if (k == kHashEmpty) break;
+          h = (h + 1u) & (kVHash - 1u);
         }
-        if (k == kHashEmpty) break;
-        h = (h + 1u) & (kVHash - 1u);
       }
     }
-    return T == 1.0f ? v : v / T;  // generate.rs:357-359 (w / 1 is w)
+    if (div_t) v = v / T;  // generate.rs:357-359
+    return v;
   };
   const StreamSrc<decltype(wval)> src{row, V, vec4, wval};
   return vocab_folds(a, b, len_b, P, L, src);
