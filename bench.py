@@ -65,22 +65,23 @@ def calibrate_copy(mib: int) -> None:
                       "copies": 10}), flush=True)
 
 
-def cpu_baseline(w, seconds: float) -> dict:
-    """Time the oracle (C++ restatement of sample_with, 1 thread, rows in
-    sequence, as the reference uses it) on rows of the same workload."""
+def cpu_baseline(w, seconds: float, threads: int = 1) -> dict:
+    """Time the oracle (C++ restatement of sample_with) on rows of the same
+    workload: with threads=1, rows in sequence as the reference uses it;
+    otherwise rows split statically over `threads` host threads."""
     from oracle import oracle  # CPU baseline leg only
 
-    rows_per_call = min(w.B, 64)
+    rows_per_call = min(w.B, 64 * threads)
     sl = slice(0, rows_per_call)
     hist = offs = None
     if w.hist is not None:
         offs = w.hist_offsets[: rows_per_call + 1].copy()
         hist = w.hist[: int(offs[-1])]
-    oracle.sample_batch(w.logits[sl], w.params, w.rng_seeds[sl], hist, offs, V=w.V, threads=1)  # warm
+    oracle.sample_batch(w.logits[sl], w.params, w.rng_seeds[sl], hist, offs, V=w.V, threads=threads)  # warm
     done = 0
     t0 = time.perf_counter()
     while True:
-        oracle.sample_batch(w.logits[sl], w.params, w.rng_seeds[sl], hist, offs, V=w.V, threads=1)
+        oracle.sample_batch(w.logits[sl], w.params, w.rng_seeds[sl], hist, offs, V=w.V, threads=threads)
         done += rows_per_call
         el = time.perf_counter() - t0
         if el >= seconds:
@@ -88,10 +89,10 @@ def cpu_baseline(w, seconds: float) -> dict:
     return {
         "value": done / el,
         "unit": "rows/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
         "sample": f"{done} rows of {w.name} (first {rows_per_call} rows repeated), "
-                  f"{el:.1f} s, 1 thread, C++ -O3 restatement of sample_with",
+                  f"{el:.1f} s, {threads} thread{'s' if threads > 1 else ''}, C++ -O3 restatement of sample_with",
     }
 
 
@@ -178,9 +179,12 @@ def main():
         except Exception:
             traffic = None
 
-    cpu = None
+    cpu = cpu_mt = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, args.cpu_seconds)
+        # The same with every host core this run may use (at most 16: the
+        # host share of one GPU on the benchmark box).
+        cpu_mt = cpu_baseline(w, args.cpu_seconds, threads=max(1, min(16, os.cpu_count() or 1)))
 
     line = {
         "metric": METRIC,
@@ -213,6 +217,7 @@ def main():
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_threads": cpu_mt,
         "parity": parity,
     }
     print(json.dumps(line), flush=True)
