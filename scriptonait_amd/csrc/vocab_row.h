@@ -44,9 +44,9 @@ namespace llmhip {
 
 constexpr uint32_t kVB = 4096;             // buckets
 constexpr float kVR = 128.0f;              // buckets per unit of y
-constexpr uint32_t kVZones = 320;          // zones per fold
+constexpr uint32_t kVZones = 320;          // zones (of either fold)
 constexpr uint32_t kVZoneEls = 4096;       // gathered elements per fold
-constexpr uint32_t kVTies = 256;           // ties in certain buckets per fold
+constexpr uint32_t kVTies = 256;           // ties in certain buckets (of either fold)
 constexpr uint32_t kVHash = 2048;          // repetition-count table slots
 constexpr uint32_t kVMaxDistinct = 1536;   // distinct history ids the table takes
 constexpr uint32_t kVBits = 4096;          // words of the history filter (bit id mod 2^17)
@@ -59,61 +59,71 @@ enum : uint8_t { kBSkip = 0, kBCert = 1, kBZone = 2, kBTie = 3 };
 
 // misc[] slots
 enum : uint32_t {
-  kVFail = 0,      // nonzero: hand the row to general_row
-  kVBeyond = 1,    // first bucket certain to lie past a stop
-  kVNTies = 2,     // ties found in certain buckets
-  kVCount = 3,     // terms >= the min-p threshold
-  kVStopPos = 4,   // fold results
-  kVStopId = 5,
-  kVStopBk = 6,
-  kVF = 7,
-  kVDistinct = 8,  // distinct history ids
-  kVCand = 9,      // min-p candidates listed
-  kVSplitDone = 10,  // waves done with the tie split
-  kVMisc = 11,
+  kVFail = 0,        // nonzero: hand the row to general_row
+  kVBeyond0 = 1,     // first bucket certain to lie past fold 0's stop
+  kVBeyond1 = 2,     // the same for fold 1
+  kVStopZone = 3,    // first bucket that may hold fold 0's stop
+  kVNTies = 4,       // ties found in certain buckets
+  kVCount = 5,       // terms >= the min-p threshold
+  kVDistinct = 6,    // distinct history ids
+  kVCand = 7,        // min-p candidates listed
+  kVSplitDone = 8,   // waves done with the tie split
+  kVKeep = 9,        // the walk's end (sorted positions kept)
+  kVRes = 10,        // fold results, 4 words per fold
+  kVMisc = 18,
 };
 
 struct VocabLds {
   uint32_t cnt[kVB];   // elements per bucket
-  float asum[kVB];     // approximate sum of x per bucket
-  uint32_t D[kVB];     // exact ulp counts of a fold's certain buckets
-  // Per bucket, one word: class << 24 | (binade + 128) << 16 | slot, the slot
-  // being the zone slot (zones) or the segment index (certain buckets).
-  uint32_t binfo[kVB];
-  // Zones in bucket order; segment z holds the certain buckets before zone z.
+  float asum[kVB];     // approximate sum of x per bucket; then fold 1's ulp counts
+  uint32_t D[kVB];     // exact ulp counts of fold 0's certain buckets
+  uint32_t binfo[kVB];  // per bucket: slot, both folds' classes and binades (bpack)
+  // Zones (buckets gathered or split at ties, for either fold) in bucket
+  // order; segment z of a fold holds its certain buckets before zone z.
   uint32_t zb[kVZones];
   uint32_t zbase[kVZones + 1];
   uint32_t zcur[kVZones];
   uint32_t zpos[kVZones];       // sorted position of the zone bucket's first element
-  int32_t zE[kVZones];          // tie zones: the bucket's binade
-  uint32_t zTub[kVZones];       // tie zones: largest term of the bucket (walk)
-  uint16_t zt0[kVZones];        // tie zones: first tie (sorted tie order), count
-  uint16_t ztn[kVZones];
-  unsigned long long seg[kVZones + 1];
-  int32_t segE[kVZones + 1];
-  uint32_t segTub[kVZones + 1];  // largest term bound of the segment (walk)
+  uint16_t zt0[2][kVZones];     // tie zones: a fold's first tie (sorted tie order), count
+  uint16_t ztn[2][kVZones];
+  unsigned long long seg[2][kVZones + 1];
+  int32_t segE[2][kVZones + 1];
+  uint32_t segTub[kVZones + 1];  // the walk: largest term bound of the segment
   // Gathered zone elements, packed as key << 32 | ~id so that a larger value
   // comes first in the reference's order; after the sort, term << 32 | ~id.
   // zperm[base + r] is the element at sorted position r of its zone. Before
   // the first fold, zpk holds the buckets' masses (amass).
   unsigned long long zpk[kVZoneEls];
   uint16_t zperm[kVZoneEls];
-  // Ties in certain buckets: key, id, ulp count, bucket; ulp sum above each.
+  // Ties in certain buckets: key, id, ulp count, fold << 31 | bucket; ulp sum
+  // above each.
   uint32_t tkey[kVTies], tidx[kVTies], tq[kVTies], tbk[kVTies], tab[kVTies];
   uint16_t tord[kVTies];
   uint32_t hkey[kVHash];
   float hval[kVHash];
-  uint32_t hbits[kVBits];  // set for every history id (mod 2^17): the table is probed only then
+  uint32_t hbits[kVBits];  // set for every history id (mod 32 * kVBits): the table is probed only then
   double scand[kWaves];
+  double amix;             // approximate mass of the bucket the min-p threshold splits
   uint32_t scanu[kWaves];
   float redf[kWaves];
   uint32_t misc[kVMisc];
   uint64_t exptab[32];
 };
 
-__device__ __forceinline__ uint32_t bcls(uint32_t bi) { return bi >> 24; }
-__device__ __forceinline__ uint32_t bslot(uint32_t bi) { return bi & 0xffffu; }
-__device__ __forceinline__ int bbinade(uint32_t bi) { return (int)((bi >> 16) & 255u) - 128; }
+// A bucket's word: slot (bits 0-8: zone slot, or segment index for certain
+// buckets), fold 0's class (9-10), fold 1's class (11-12), step bits (13-14),
+// fold 0's binade + 128 (16-23), fold 1's binade + 128 (24-31). Step bit f:
+// the bucket is gathered and certain for fold f, but holds a tie for it, so
+// fold f replays it element by element rather than adding its ulp count.
+static_assert(kVZones < 512, "slot bits");
+constexpr uint32_t kBStep = 1u << 13;
+__device__ __forceinline__ uint32_t bpack(uint32_t slot, uint32_t c0, uint32_t c1, int e0, int e1) {
+  return slot | (c0 << 9) | (c1 << 11) | ((uint32_t)(e0 + 128) << 16) | ((uint32_t)(e1 + 128) << 24);
+}
+__device__ __forceinline__ uint32_t bcls_shift(int f) { return 9u + 2u * (uint32_t)f; }
+__device__ __forceinline__ uint32_t bcls(uint32_t bi, int f) { return (bi >> bcls_shift(f)) & 3u; }
+__device__ __forceinline__ uint32_t bslot(uint32_t bi) { return bi & 511u; }
+__device__ __forceinline__ int bbin(uint32_t bi, int f) { return (int)((bi >> (16 + 8 * f)) & 255u) - 128; }
 
 __device__ __forceinline__ uint32_t vbucket(float y) {
   const float ny = -y;
@@ -264,15 +274,15 @@ __device__ __forceinline__ float cheap_x(float y) {
   return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(f), (int)kf);
 }
 
-// One fold over the row's terms in sorted order (see the file comment).
+// One or two folds over the row's terms in sorted order (see the file
+// comment). Two folds (the top-p cumulative and the walk, which take the same
+// terms) share the classification's layout, the exact pass, the tie split and
+// the zone sort; only their replays are separate.
 struct FoldSpec {
-  float F0;          // starting value
+  float F0;          // starting value (the walk: set by run_folds)
   float S;           // terms are x / S (0: the terms are x)
   float thr;         // terms below thr are outside the fold (min-p); <= 0: none
   float stop_ge;     // add folds: stop at the first F >= stop_ge
-  uint32_t kend;     // buckets >= kend are outside the fold
-  uint32_t kpart;    // bucket whose positions >= pos_end are outside (or kVB)
-  uint32_t pos_end;  // sorted positions >= pos_end are outside
   bool sub;          // the walk: stop before t when F < t, else F -= t
 };
 
@@ -288,21 +298,39 @@ __device__ __forceinline__ bool before(uint32_t ka, uint32_t ia, uint32_t kb, ui
   return ka > kb || (ka == kb && ia < ib);
 }
 
-template <class Src>
-__device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds& L, const Src& src, FoldRes& res,
-                                         uint32_t* status) {
+// NF == 1: fs[0] only. NF == 2: fs[0] is the top-p cumulative and fs[1] the
+// walk; the walk's start is u * (fold 0's result), and while the two are
+// classified it is only known to lie in an interval, which the walk's margin
+// covers. The walk ends at sorted position keep (returned in keep_out): fold
+// 0's cut + 1, or without a cut the number of terms >= thr (at least 1) when
+// keep_count, else keep_default.
+template <int NF, class Src>
+__device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u, uint32_t keep_default, bool keep_count,
+                                          VocabLds& L, const Src& src, FoldRes (&res)[NF], uint32_t& keep_out,
+                                          uint32_t* status) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t k0 = tid * 4u;
-  const double scale = fs.S > 0.0f ? 1.0 / (double)fs.S : 1.0;
-  auto term_of = [&](float x) __attribute__((always_inline)) { return fs.S > 0.0f ? x / fs.S : x; };
+  const float S = fs[0].S, thr = fs[0].thr;  // the same terms for both folds
+  const double scale = S > 0.0f ? 1.0 / (double)S : 1.0;
+  auto term_of = [&](float x) __attribute__((always_inline)) { return S > 0.0f ? x / S : x; };
+  // Fold 1's exact ulp counts live where the approximate masses were: those
+  // are no longer needed once both folds are classified.
+  uint32_t* Dw = reinterpret_cast<uint32_t*>(L.asum);
+  auto Df = [&](int f) __attribute__((always_inline)) -> uint32_t* { return f == 0 ? L.D : Dw; };
 
   for (uint32_t s = tid; s <= kVZones; s += kBlock) {
-    L.seg[s] = 0ull;
-    L.segE[s] = kNoE;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      L.seg[f][s] = 0ull;
+      L.segE[f][s] = kNoE;
+    }
     L.segTub[s] = 0u;
   }
   if (tid == 0) {
-    L.misc[kVBeyond] = kVB;
+    L.amix = 0.0;
+    L.misc[kVBeyond0] = kVB;
+    L.misc[kVBeyond1] = kVB;
+    L.misc[kVStopZone] = kVB;
     L.misc[kVNTies] = 0u;
     L.misc[kVCount] = 0u;
     L.misc[kVSplitDone] = 0u;
@@ -314,9 +342,9 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
   // consequence exactly, so a wrong guess costs a hand-over, not an id.
   uint32_t c4[4];
   double a4[4];
-  float tub4[4];
-  uint8_t cl[4];
-  int e4[4] = {0, 0, 0, 0};
+  float tub4[4], tlb4[4];
+  uint8_t cl[2][4];
+  int e4[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
   uint32_t cs = 0;
   double as = 0.0;
 #pragma unroll
@@ -324,9 +352,11 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
     const uint32_t k = k0 + j;
     c4[j] = L.cnt[k];
     tub4[j] = term_of(glibc_expf_tab(-(float)k / kVR, L.exptab));
-    const bool out = !c4[j] || k >= fs.kend || (fs.thr > 0.0f && tub4[j] < fs.thr);
+    tlb4[j] = k + 1 < kVB ? term_of(glibc_expf_tab(-(float)(k + 1) / kVR, L.exptab)) : 0.0f;
+    const bool out = !c4[j] || (thr > 0.0f && tub4[j] < thr);
     a4[j] = out ? 0.0 : (double)L.asum[k] * scale;
-    cl[j] = out ? kBSkip : kBCert;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) cl[f][j] = (out || f >= NF) ? kBSkip : kBCert;
     cs += c4[j];
     as += a4[j];
   }
@@ -334,58 +364,104 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
   const uint32_t cpre = block_scan_u32(cs, L.scanu, ctot);
   double atot;
   const double apre = block_scan_f64(as, L.scand, atot);
-  {
-    const double sg = fs.sub ? -1.0 : 1.0;
+  // The one bucket that the min-p threshold splits: its mass counts in full
+  // above, but only part of it is in the folds.
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (a4[j] > 0.0 && thr > 0.0f && tlb4[j] < thr) L.amix = a4[j];
+  // One fold's classes for this thread's buckets. kend: buckets from there
+  // on are outside the fold. err0: a margin added to every interval.
+  auto classify = [&](int f, const FoldSpec& sp, uint32_t kend, double err0, uint32_t beyond_slot)
+      __attribute__((always_inline)) {
+    const double sg = sp.sub ? -1.0 : 1.0;
     uint32_t nb = cpre;
     double P = apre;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t k = k0 + j;
-      const double Ga = fs.F0 + sg * P, Gb = fs.F0 + sg * (P + a4[j]);
-      if (cl[j] != kBSkip) {
-        const float tlb = k + 1 < kVB ? term_of(glibc_expf_tab(-(float)(k + 1) / kVR, L.exptab)) : 0.0f;
-        if (k == 0 || k == fs.kpart || (fs.thr > 0.0f && tlb < fs.thr)) {
-          cl[j] = kBZone;
+      const double Ga = sp.F0 + sg * P, Gb = sp.F0 + sg * (P + a4[j]);
+      if (k >= kend) cl[f][j] = kBSkip;
+      if (cl[f][j] != kBSkip) {
+        // Bucket 0 and the bucket that the min-p threshold splits are always
+        // gathered.
+        const bool forced = k == 0 || (thr > 0.0f && tlb4[j] < thr);
+        double hi = fmax(Ga, Gb), lo = fmin(Ga, Gb);
+        const double err = (6.0 * sqrt((double)nb + 1.0) * 0x1p-24 + 0x1p-20) * (sp.sub ? (double)sp.F0 : hi) + err0;
+        if (!forced && ((!sp.sub && Ga - err >= (double)sp.stop_ge) || (sp.sub && Ga + err < 0.0))) {
+          cl[f][j] = kBSkip;
+          atomicMin(&L.misc[beyond_slot], k);
         } else {
-          double hi = fmax(Ga, Gb), lo = fmin(Ga, Gb);
-          const double err = (6.0 * sqrt((double)nb + 1.0) * 0x1p-24 + 0x1p-20) * (fs.sub ? (double)fs.F0 : hi);
-          if ((!fs.sub && Ga - err >= (double)fs.stop_ge) || (fs.sub && Ga + err < 0.0)) {
-            cl[j] = kBSkip;
-            atomicMin(&L.misc[kVBeyond], k);
+          lo -= err;
+          hi += err;
+          const bool stopz = !sp.sub && hi >= (double)sp.stop_ge;
+          if (stopz && f == 0) atomicMin(&L.misc[kVStopZone], k);  // the cut can first fall here
+          const int E = lo > 0.0 ? dbinade(lo) : 0;
+          if (forced || stopz || !(lo > 0.0) || E != dbinade(hi) || E < -120 || E > 120 ||
+              (sp.sub && lo <= (double)tub4[j] * (1.0 + 0x1p-20))) {
+            cl[f][j] = kBZone;
           } else {
-            lo -= err;
-            hi += err;
-            const int E = lo > 0.0 ? dbinade(lo) : 0;
-            if (!(lo > 0.0) || E != dbinade(hi) || E < -120 || E > 120 || (!fs.sub && hi >= (double)fs.stop_ge) ||
-                (fs.sub && lo <= (double)tub4[j] * (1.0 + 0x1p-20))) {
-              cl[j] = kBZone;
-            } else {
-              e4[j] = E;
-            }
+            e4[f][j] = E;
           }
         }
       }
       nb += c4[j];
       P += a4[j];
     }
-  }
+  };
+  classify(0, fs[0], kVB, 0.0, kVBeyond0);
   __syncthreads();
-  const uint32_t kb = L.misc[kVBeyond];
+  const uint32_t kb0 = L.misc[kVBeyond0];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (k0 + j >= kb) cl[j] = kBSkip;
+    if (k0 + j >= kb0) cl[0][j] = kBSkip;
+  uint32_t kb1 = kVB;
+  if constexpr (NF == 2) {
+    // The walk starts at u * total, total being fold 0's value where it ends.
+    // At a cut, total lies in [stop_ge, stop_ge + the largest term of the
+    // first bucket that can hold the cut]; without one, it is the sum of all
+    // the fold's terms, which the approximate masses bound. The walk is
+    // classified for any start in that range (its margin covers the range);
+    // the replay then starts from the exact value and checks everything.
+    const uint32_t ksz = L.misc[kVStopZone];
+    const double stop_ge = (double)fs[0].stop_ge;
+    double tlo = INFINITY, thi = -INFINITY;
+    if (ksz < kVB) {
+      const double tmax = (double)term_of(glibc_expf_tab(-(float)ksz / kVR, L.exptab));
+      tlo = stop_ge;
+      thi = stop_ge + tmax * (1.0 + 0x1p-20) + stop_ge * 0x1p-23;
+    }
+    const double e = (6.0 * sqrt((double)ctot + 1.0) * 0x1p-24 + 0x1p-20) * atot;
+    if (!(atot - L.amix - e >= stop_ge)) {  // the fold may end without a cut
+      tlo = fmin(tlo, atot - L.amix - e);
+      thi = fmax(thi, fmin(atot + e, stop_ge));
+    }
+    if (!(tlo <= thi) || !(thi < 0x1p100)) return false;
+    const double r0_lo = (double)u * tlo * (1.0 - 0x1p-22), r0_hi = (double)u * thi * (1.0 + 0x1p-22);
+    fs[1].F0 = (float)(0.5 * (r0_lo + r0_hi));
+    classify(1, fs[1], kb0, 0.5 * (r0_hi - r0_lo) + (double)fs[1].F0 * 0x1p-23, kVBeyond1);
+    __syncthreads();
+    kb1 = L.misc[kVBeyond1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (k0 + j >= kb1) cl[1][j] = kBSkip;
+  }
 
-  // Zone slots, segment indices and element bases, in bucket order. Run a
-  // second time when ties made certain buckets into tie zones: those hold no
-  // elements, so every gathering zone keeps its element base, and its
-  // gathered count is carried over in D[bucket].
+  // Zone slots, segment indices and element bases, in bucket order. A bucket
+  // is a gathering zone when it is a zone for either fold, a tie zone when it
+  // holds a tie of either fold, and otherwise belongs to the segment before
+  // the next zone. Run a second time when ties turned certain buckets into
+  // tie zones: those hold no elements, so every gathering zone keeps its
+  // element base, and its gathered count and step bits are carried over.
   uint32_t nz = 0;
-  auto layout = [&](bool again) __attribute__((always_inline)) -> bool {
+  uint32_t carry4[4] = {0u, 0u, 0u, 0u};  // a gathering bucket's count and step bits, across a re-layout
+  auto gathers = [&](int j) __attribute__((always_inline)) { return cl[0][j] == kBZone || cl[1][j] == kBZone; };
+  auto ties_in = [&](int j) __attribute__((always_inline)) { return cl[0][j] == kBTie || cl[1][j] == kBTie; };
+  auto layout = [&]() __attribute__((always_inline)) -> bool {
     uint32_t zc = 0, ze = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      zc += (cl[j] == kBZone || cl[j] == kBTie) ? 1u : 0u;
-      ze += cl[j] == kBZone ? c4[j] : 0u;
+      zc += (gathers(j) || ties_in(j)) ? 1u : 0u;
+      ze += gathers(j) ? c4[j] : 0u;
     }
     uint32_t nel;
     uint32_t zi = block_scan_u32(zc, L.scanu, nz);
@@ -395,94 +471,109 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t k = k0 + j;
-      if (cl[j] == kBZone || cl[j] == kBTie) {
-        L.binfo[k] = ((uint32_t)cl[j] << 24) | ((uint32_t)(e4[j] + 128) << 16) | zi;
+      const bool zone = gathers(j) || ties_in(j);
+      L.binfo[k] = bpack(zi, cl[0][j], cl[1][j], e4[0][j], e4[1][j]) | (carry4[j] & (kBStep * 3u));
+      if (zone) {
         L.zb[zi] = k;
         L.zbase[zi] = ei;
-        L.zcur[zi] = again && cl[j] == kBZone ? L.D[k] : 0u;
+        L.zcur[zi] = carry4[j] & (kBStep - 1u);
         L.zpos[zi] = pos;
-        L.zE[zi] = e4[j];
-        L.zTub[zi] = __float_as_uint(tub4[j]);
         ++zi;
-        if (cl[j] == kBZone) ei += c4[j];
-      } else if (cl[j] == kBCert) {
-        L.binfo[k] = ((uint32_t)cl[j] << 24) | ((uint32_t)(e4[j] + 128) << 16) | zi;
-        L.segE[zi] = e4[j];
-        atomicMax(&L.segTub[zi], __float_as_uint(tub4[j]));
+        if (gathers(j)) ei += c4[j];
+      } else {
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          if (cl[f][j] == kBCert) {
+            L.segE[f][zi] = e4[f][j];
+            if (fs[f].sub) atomicMax(&L.segTub[zi], __float_as_uint(tub4[j]));
+          }
       }
-      if (cl[j] == kBSkip) L.binfo[k] = 0u;
       pos += c4[j];
     }
     if (tid == 0) L.zbase[nz] = nel;
     return true;
   };
-  if (!layout(false)) return false;
+  if (!layout()) return false;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) L.D[k0 + j] = 0u;
+  for (int j = 0; j < 4; ++j) {
+    L.D[k0 + j] = 0u;
+    if constexpr (NF == 2) Dw[k0 + j] = 0u;
+  }
   __syncthreads();
 
   // Exact pass: certain buckets add ulp counts, zones gather, ties are listed.
   // A term is first taken from a cheap exp (cheap_x: within 2^-22 of glibc's
   // expf, and after the reciprocal multiply within 2^-20 of the exact term);
   // the exact term is computed only when the cheap one cannot settle the
-  // min-p test or the ulp count (a scaled value within value * 2^-20 of a
+  // min-p test or an ulp count (a scaled value within value * 2^-20 of a
   // half-integer, or a term near the binade).
-  const float rcpS = fs.S > 0.0f ? 1.0f / fs.S : 1.0f;
+  const float rcpS = S > 0.0f ? 1.0f / S : 1.0f;
   uint32_t nin = 0;
   src.for_each([&](float w, uint32_t i) __attribute__((always_inline)) {
     const float y = w - mx;
     const uint32_t k = vbucket(y);
     const uint32_t bi = L.binfo[k];
-    const uint32_t c = bcls(bi);
-    if (c == kBSkip) return;
+    const uint32_t c0 = bcls(bi, 0), c1 = bcls(bi, 1);
+    if (c0 == kBSkip && c1 == kBSkip) return;
     const bool cheap = y >= -80.0f;
     const float ta = cheap ? cheap_x(y) * rcpS : 0.0f;
     float t = -1.0f;  // the exact term, once computed
-    if (fs.thr > 0.0f) {
+    if (thr > 0.0f) {
       bool in;
-      if (cheap && ta >= fs.thr * (1.0f + 0x1p-19f)) {
+      if (cheap && ta >= thr * (1.0f + 0x1p-19f)) {
         in = true;
-      } else if (cheap && ta < fs.thr * (1.0f - 0x1p-19f)) {
+      } else if (cheap && ta < thr * (1.0f - 0x1p-19f)) {
         in = false;
       } else {
         t = term_of(glibc_expf_tab(y, L.exptab));
-        in = t >= fs.thr;
+        in = t >= thr;
       }
       if (!in) return;
     }
-    ++nin;
-    if (c == kBZone) {
+    if (c0 != kBSkip) ++nin;
+    // A gathered bucket that is certain for the other fold is also counted
+    // for it, so that fold adds it as one integer.
+    const bool gath = c0 == kBZone || c1 == kBZone;
+    if (gath) {
       const uint32_t z = bslot(bi);
       const uint32_t e = L.zbase[z] + atomicAdd(&L.zcur[z], 1u);
       L.zpk[e] = ((unsigned long long)f2key(w) << 32) | (uint32_t)~i;
-      return;
+      if constexpr (NF == 1) return;
     }
-    const int E = bbinade(bi);
-    if (cheap && t < 0.0f) {
-      const float v = __builtin_amdgcn_ldexpf(ta, 23 - E);  // ta in units of 2^(E-23), exactly
-      if (v < 0x1p22f) {
-        const float fl = floorf(v), fr = v - fl;
-        if (fabsf(fr - 0.5f) > v * 0x1p-20f + 0x1p-40f) {
-          atomicAdd(&L.D[k], (uint32_t)fl + (fr > 0.5f ? 1u : 0u));
-          return;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      if ((f == 0 ? c0 : c1) != kBCert) continue;
+      const int E = bbin(bi, f);
+      if (cheap && t < 0.0f) {
+        const float v = __builtin_amdgcn_ldexpf(ta, 23 - E);  // ta in units of 2^(E-23), exactly
+        if (v < 0x1p22f) {
+          const float fl = floorf(v), fr = v - fl;
+          if (fabsf(fr - 0.5f) > v * 0x1p-20f + 0x1p-40f) {
+            atomicAdd(&Df(f)[k], (uint32_t)fl + (fr > 0.5f ? 1u : 0u));
+            continue;
+          }
         }
       }
-    }
-    if (t < 0.0f) t = term_of(glibc_expf_tab(y, L.exptab));
-    bool tie, big;
-    const uint32_t q = rne_units(t, E, tie, big);
-    if (big) L.misc[kVFail] = 1u;
-    if (tie) {
-      const uint32_t s = atomicAdd(&L.misc[kVNTies], 1u);
-      if (s < kVTies) {
-        L.tkey[s] = f2key(w);
-        L.tidx[s] = i;
-        L.tq[s] = q;
-        L.tbk[s] = k;
-        L.tab[s] = 0u;
+      if (t < 0.0f) t = term_of(glibc_expf_tab(y, L.exptab));
+      bool tie, big;
+      const uint32_t q = rne_units(t, E, tie, big);
+      if (gath && (tie || big)) {
+        atomicOr(&L.binfo[k], kBStep << f);  // this fold replays the bucket element by element
+        continue;
       }
-    } else {
-      atomicAdd(&L.D[k], q);
+      if (big) L.misc[kVFail] = 1u;
+      if (tie) {
+        const uint32_t s = atomicAdd(&L.misc[kVNTies], 1u);
+        if (s < kVTies) {
+          L.tkey[s] = f2key(w);
+          L.tidx[s] = i;
+          L.tq[s] = q;
+          L.tbk[s] = k | ((uint32_t)f << 31);
+          L.tab[s] = 0u;
+        }
+      } else {
+        atomicAdd(&Df(f)[k], q);
+      }
     }
   });
   nin = wave_sum(nin);
@@ -492,59 +583,71 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
   if (L.misc[kVFail] || nt > kVTies) return false;
 
   if (nt) {
-    // Ties in certain buckets: sort them by (bucket, key desc, id asc), make
-    // their buckets tie zones, and sum each bucket's ulp counts above each
-    // tie.
+    // Ties in certain buckets: sort them by (fold, bucket, key desc, id asc),
+    // make their buckets tie zones of their fold, and (below) sum each
+    // bucket's ulp counts above each tie.
     for (uint32_t s = tid; s < nt; s += kBlock) {
       uint32_t r = 0;
       const uint32_t bs = L.tbk[s], ks = L.tkey[s], is = L.tidx[s];
-      for (uint32_t u = 0; u < nt; ++u) {
-        const uint32_t bu = L.tbk[u];
-        r += (bu < bs || (bu == bs && before(L.tkey[u], L.tidx[u], ks, is))) ? 1u : 0u;
+      for (uint32_t v = 0; v < nt; ++v) {
+        const uint32_t bu = L.tbk[v];
+        r += (bu < bs || (bu == bs && before(L.tkey[v], L.tidx[v], ks, is))) ? 1u : 0u;
       }
       L.tord[r] = (uint16_t)s;
+      const uint32_t f = bs >> 31;
+      atomicOr(&L.binfo[bs & 0x7fffffffu], (uint32_t)(kBTie ^ kBCert) << bcls_shift(f));  // CERT -> TIE
     }
-    for (uint32_t s = tid; s < nt; s += kBlock) {
-      const uint32_t k = L.tbk[s];  // every tie of a bucket writes the same word
-      L.binfo[k] = (L.binfo[k] & 0x00ffffffu) | ((uint32_t)kBTie << 24);
-    }
-    for (uint32_t z = tid; z < nz; z += kBlock)
-      if (bcls(L.binfo[L.zb[z]]) == kBZone) L.D[L.zb[z]] = L.zcur[z];
     for (uint32_t s = tid; s <= kVZones; s += kBlock) {
-      L.segE[s] = kNoE;
+#pragma unroll
+      for (int f = 0; f < 2; ++f) L.segE[f][s] = kNoE;
       L.segTub[s] = 0u;
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (bcls(L.binfo[k0 + j]) == kBTie) cl[j] = kBTie;
-    if (!layout(true)) return false;
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t bi = L.binfo[k0 + j];
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        if (bcls(bi, f) == kBTie) cl[f][j] = kBTie;
+      carry4[j] = gathers(j) ? L.zcur[bslot(bi)] | (bi & (kBStep * 3u)) : 0u;
+    }
+    if (!layout()) return false;
     __syncthreads();
     for (uint32_t z = tid; z < nz; z += kBlock) {
       const uint32_t k = L.zb[z];
-      if (bcls(L.binfo[k]) != kBTie) continue;
-      uint32_t lo = 0, hi = nt;  // the bucket's ties are a run of tord
-      while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (L.tbk[L.tord[mid]] < k) lo = mid + 1; else hi = mid;
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        L.zt0[f][z] = 0u;
+        L.ztn[f][z] = 0u;
+        if (f >= NF || bcls(L.binfo[k], f) != kBTie) continue;
+        const uint32_t key = k | ((uint32_t)f << 31);
+        uint32_t lo = 0, hi = nt;  // a fold's ties in a bucket are a run of tord
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (L.tbk[L.tord[mid]] < key) lo = mid + 1; else hi = mid;
+        }
+        uint32_t e = lo;
+        while (e < nt && L.tbk[L.tord[e]] == key) ++e;
+        L.zt0[f][z] = (uint16_t)lo;
+        L.ztn[f][z] = (uint16_t)(e - lo);
       }
-      uint32_t e = lo;
-      while (e < nt && L.tbk[L.tord[e]] == k) ++e;
-      L.zt0[z] = (uint16_t)lo;
-      L.ztn[z] = (uint16_t)(e - lo);
     }
     __syncthreads();
   }
 
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (cl[j] == kBCert) atomicAdd(&L.seg[bslot(L.binfo[k0 + j])], (unsigned long long)L.D[k0 + j]);
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      if (cl[f][j] == kBCert && !gathers(j) && !ties_in(j))
+        atomicAdd(&L.seg[f][bslot(L.binfo[k0 + j])], (unsigned long long)Df(f)[k0 + j]);
 
   // Sort each gathering zone by (key desc, id asc), ranking by counting
   // larger packed values; then replace each key by the element's term, so
-  // the replay reads terms.
+  // the replays read terms.
   for (uint32_t z = wave; z < nz; z += kWaves) {
-    if (bcls(L.binfo[L.zb[z]]) != kBZone) continue;
+    const uint32_t bz = L.binfo[L.zb[z]];
+    if (bcls(bz, 0) != kBZone && bcls(bz, 1) != kBZone) continue;
     const uint32_t base = L.zbase[z], n = L.zcur[z];
     const unsigned long long* pk = L.zpk + base;
     for (uint32_t i = lane; i < n; i += 64u) {
@@ -572,196 +675,245 @@ __device__ __forceinline__ bool run_fold(const FoldSpec& fs, float mx, VocabLds&
       const float y = w - mx;
       const uint32_t k = vbucket(y);
       const uint32_t bi = L.binfo[k];
-      if (bcls(bi) != kBTie) return;
+      if (bcls(bi, 0) != kBTie && bcls(bi, 1) != kBTie) return;
       const float t = term_of(glibc_expf_tab(y, L.exptab));
-      if (fs.thr > 0.0f && !(t >= fs.thr)) return;
+      if (thr > 0.0f && !(t >= thr)) return;
       const uint32_t z = bslot(bi);
-      bool tie, big;
-      const uint32_t q = rne_units(t, bbinade(bi), tie, big);
-      if (tie || q == 0u) return;
       const uint32_t key = f2key(w);
-      const uint32_t t0 = L.zt0[z], tn = L.ztn[z];
-      for (uint32_t u = 0; u < tn; ++u) {
-        const uint32_t s = L.tord[t0 + u];
-        if (before(key, i, L.tkey[s], L.tidx[s])) atomicAdd(&L.tab[s], q);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        if (bcls(bi, f) != kBTie) continue;
+        bool tie, big;
+        const uint32_t q = rne_units(t, bbin(bi, f), tie, big);
+        if (tie || q == 0u) continue;
+        const uint32_t t0 = L.zt0[f][z], tn = L.ztn[f][z];
+        for (uint32_t v = 0; v < tn; ++v) {
+          const uint32_t s = L.tord[t0 + v];
+          if (before(key, i, L.tkey[s], L.tidx[s])) atomicAdd(&L.tab[s], q);
+        }
       }
     }, 64u, kBlock - 64u);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     if (lane == 0) atomicAdd(&L.misc[kVSplitDone], 1u);
   }
 
-  // Replay (wave 0): certain segments as integers, tie zones split at their
-  // ties, gathering zones 64 elements at a time.
+  // Replays (wave 0), one fold after the other: certain segments as
+  // integers, tie zones split at their ties, gathering zones 64 elements at a
+  // time.
   if (wave == 0) {
     bool split_ready = nt == 0u;
-    float F = fs.F0;
-    bool fail = false, stopped = false;
-    uint32_t stop_pos = kNoPos, stop_id = 0, stop_bk = 0;
-    // Adds d ulps to F in binade E (add folds) or takes them away (the walk);
-    // false when F would leave the binade.
-    auto apply_units = [&](int E, uint64_t d) __attribute__((always_inline)) -> bool {
-      const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
-      if (!(F > 0.0f) || ef == 0u || ef == 255u || (int)ef - 127 != E) return false;
-      uint64_t M = (fb & 0x7fffffu) | 0x800000u;
-      if (!fs.sub) {
-        M += d;
-        if (M >= (1ull << 24)) return false;
-      } else {
-        if (M < d + (1ull << 23) + 1ull) return false;
-        M -= d;
-      }
-      F = from_units((uint32_t)M, E);
-      return true;
-    };
-    // One element in f32, the reference's way; true when the fold stops.
-    auto step = [&](float tv) __attribute__((always_inline)) -> bool {
-      if (fs.sub) {
-        if (F < tv) return true;
-        F = F - tv;
-        return false;
-      }
-      F = F + tv;
-      return F >= fs.stop_ge;
-    };
-    for (uint32_t zc = 0; zc <= nz && !fail && !stopped; zc += 64u) {
-      // Segment and zone data of zones zc .. zc + 63, one zone per lane, so
-      // the walk through them reads registers.
-      const uint32_t zl = zc + lane;
-      uint32_t mSegE = (uint32_t)kNoE, mSegTub = 0u, mK = 0u, mBase = 0u, mN = 0u, mP0 = 0u, mCls = 0u;
-      uint32_t mE = 0u, mTub = 0u, mT0 = 0u, mTn = 0u, mD = 0u;
-      uint64_t mSeg = 0ull;
-      if (zl <= nz) {
-        mSegE = (uint32_t)L.segE[zl];
-        mSeg = L.seg[zl];
-        mSegTub = L.segTub[zl];
-      }
-      if (zl < nz) {
-        mK = L.zb[zl];
-        mBase = L.zbase[zl];
-        mN = L.zcur[zl];
-        mP0 = L.zpos[zl];
-        mCls = bcls(L.binfo[mK]);
-        mE = (uint32_t)L.zE[zl];
-        mTub = L.zTub[zl];
-        mT0 = L.zt0[zl];
-        mTn = L.ztn[zl];
-        mD = L.D[mK];
-      }
-      for (uint32_t zi = 0; zi < 64u && zc + zi <= nz && !fail && !stopped; ++zi) {
-        const uint32_t z = zc + zi;
-        const int Es = (int)readlane_u32(mSegE, zi);
-        if (Es != kNoE) {
-          if (!apply_units(Es, readlane_u64(mSeg, zi))) fail = true;
-          else if (!fs.sub && F >= fs.stop_ge) fail = true;
-          else if (fs.sub && F < __uint_as_float(readlane_u32(mSegTub, zi))) fail = true;
+    bool fail = false;
+    uint32_t keep = keep_default;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      if (fail) break;
+      const FoldSpec& sp = fs[f];
+      const uint32_t kb = f == 0 ? kb0 : kb1;
+      const uint32_t pos_end = f == 0 ? kNoPos : keep;
+      float F = sp.F0;
+      if (f == 1) F = u * res[0].F;  // generate.rs:411-412: r = u * total
+      bool stopped = false;  // a stop, the end at keep, or past the last bucket
+      bool at_keep = false;
+      uint32_t stop_pos = kNoPos, stop_id = 0, stop_bk = 0;
+      // Adds d ulps to F in binade E (add folds) or takes them away (the
+      // walk); false when F would leave the binade.
+      auto apply_units = [&](int E, uint64_t d) __attribute__((always_inline)) -> bool {
+        const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
+        if (!(F > 0.0f) || ef == 0u || ef == 255u || (int)ef - 127 != E) return false;
+        uint64_t M = (fb & 0x7fffffu) | 0x800000u;
+        if (!sp.sub) {
+          M += d;
+          if (M >= (1ull << 24)) return false;
+        } else {
+          if (M < d + (1ull << 23) + 1ull) return false;
+          M -= d;
         }
-        if (z == nz || fail) break;
-        const uint32_t k = readlane_u32(mK, zi);
-        if (readlane_u32(mCls, zi) == kBTie) {
-          if (!split_ready) {
-            lds_wait(&L.misc[kVSplitDone], kWaves - 1u, status);
-            split_ready = true;
-          }
-          const int E = (int)readlane_u32(mE, zi);
-          uint32_t prev = 0;
-          const uint32_t t0 = readlane_u32(mT0, zi), tn = readlane_u32(mTn, zi);
-          for (uint32_t u = 0; u < tn && !fail; ++u) {
-            const uint32_t s = L.tord[t0 + u];
-            const uint32_t ab = L.tab[s];
-            if (!apply_units(E, ab - prev)) fail = true;
-            prev = ab;
-            const uint32_t q = L.tq[s];
-            const uint32_t par = (__float_as_uint(F) ^ q) & 1u;  // parity of M - q or M + q
-            if (!fail && !apply_units(E, (uint64_t)q + par)) fail = true;
-          }
-          if (!fail && !apply_units(E, readlane_u32(mD, zi) - prev)) fail = true;
-          if (!fail && !fs.sub && F >= fs.stop_ge) fail = true;
-          if (!fail && fs.sub && F < __uint_as_float(readlane_u32(mTub, zi))) fail = true;
-          continue;
+        F = from_units((uint32_t)M, E);
+        return true;
+      };
+      // One element in f32, the reference's way; true when the fold stops.
+      auto step = [&](float tv) __attribute__((always_inline)) -> bool {
+        if (sp.sub) {
+          if (F < tv) return true;
+          F = F - tv;
+          return false;
         }
-        const uint32_t base = readlane_u32(mBase, zi), n = readlane_u32(mN, zi), p0 = readlane_u32(mP0, zi);
-        uint32_t r0 = 0;
-        while (r0 < n && !stopped) {
-          const uint32_t r = r0 + lane;
-          float t = 0.0f;
-          uint32_t id = 0u;
-          if (r < n) {
-            const unsigned long long v = L.zpk[base + L.zperm[base + r]];
-            t = __uint_as_float((uint32_t)(v >> 32));
-            id = ~(uint32_t)v;
+        F = F + tv;
+        return F >= sp.stop_ge;
+      };
+      for (uint32_t zc = 0; zc <= nz && !fail && !stopped; zc += 64u) {
+        // Segment and zone data of zones zc .. zc + 63, one zone per lane, so
+        // the walk through them reads registers.
+        const uint32_t zl = zc + lane;
+        uint32_t mSegE = (uint32_t)kNoE, mSegTub = 0u, mK = 0u, mBase = 0u, mN = 0u, mP0 = 0u, mBi = 0u;
+        uint32_t mTub = 0u, mT0 = 0u, mTn = 0u, mD = 0u;
+        uint64_t mSeg = 0ull;
+        if (zl <= nz) {
+          mSegE = (uint32_t)L.segE[f][zl];
+          mSeg = L.seg[f][zl];
+          if (sp.sub) mSegTub = L.segTub[zl];
+        }
+        if (zl < nz) {
+          mK = L.zb[zl];
+          mBase = L.zbase[zl];
+          mN = L.zcur[zl];
+          mP0 = L.zpos[zl];
+          mBi = L.binfo[mK];
+          if (sp.sub) mTub = __float_as_uint(term_of(glibc_expf_tab(-(float)mK / kVR, L.exptab)));  // largest term of the bucket
+          mT0 = L.zt0[f][zl];
+          mTn = L.ztn[f][zl];
+          mD = Df(f)[mK];
+        }
+        for (uint32_t zi = 0; zi < 64u && zc + zi <= nz && !fail && !stopped; ++zi) {
+          const uint32_t z = zc + zi;
+          const int Es = (int)readlane_u32(mSegE, zi);
+          if (Es != kNoE) {
+            if (!apply_units(Es, readlane_u64(mSeg, zi))) fail = true;
+            else if (!sp.sub && F >= sp.stop_ge) fail = true;
+            else if (sp.sub && F < __uint_as_float(readlane_u32(mSegTub, zi))) fail = true;
           }
-          const bool live = r < n;
-          const bool past = live && p0 + r >= fs.pos_end;
-          const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
-          uint32_t ev_lane = 0u;  // first lane stepped in f32
-          uint32_t done = 0u;     // lanes before it, folded as integers
-          if (F > 0.0f && ef >= 1u && ef <= 254u) {
-            const int E = (int)ef - 127;
-            const uint32_t M = (fb & 0x7fffffu) | 0x800000u;
-            bool tie = false, big = false;
-            const uint32_t q = live && !past ? rne_units(t, E, tie, big) : 0u;
-            const uint32_t incl = wave_incl_scan(q), excl = incl - q;
-            bool ev;
-            if (!fs.sub) {
-              const uint64_t Mi = (uint64_t)M + incl;
-              ev = tie || big || Mi >= (1ull << 24) || from_units((uint32_t)Mi, E) >= fs.stop_ge;
-            } else {
-              const bool ub = (uint64_t)excl + (1ull << 23) + 1ull > M;
-              const bool ui = (uint64_t)incl + (1ull << 23) + 1ull > M;
-              ev = tie || big || ub || ui || from_units(M - excl, E) < t;
-            }
-            ev = live && (ev || past);
-            const uint64_t m = __ballot(ev);
-            ev_lane = m ? (uint32_t)__ffsll((unsigned long long)m) - 1u : 64u;
-            done = min(ev_lane, n - r0);
-            if (done) {
-              const uint32_t sum = readlane_u32(incl, done - 1u);
-              const uint64_t M2 = fs.sub ? (uint64_t)M - sum : (uint64_t)M + sum;
-              F = from_units((uint32_t)M2, E);
-            }
-          }
-          if (r0 + done >= n) {
-            r0 = n;
-            break;
-          }
-          if (done == 64u) {  // no event in these 64
-            r0 += 64u;
-            continue;
-          }
-          // Element ev_lane (or the first one when F is not a normal number).
-          const uint32_t le = done;
-          const uint32_t pos = p0 + r0 + le;
-          if (pos >= fs.pos_end) {
-            stopped = true;  // the rest of the fold is outside it
-            break;
-          }
-          if (step(readlane_f32(t, le))) {
-            stop_pos = pos;
-            stop_id = readlane_u32(id, le);
-            stop_bk = k;
+          if (z == nz || fail) break;
+          const uint32_t k = readlane_u32(mK, zi);
+          if (k >= kb) {  // past the fold's last bucket
             stopped = true;
             break;
           }
-          r0 += le + 1u;
+          const uint32_t bi = readlane_u32(mBi, zi);
+          const uint32_t cf = bcls(bi, f);
+          if (cf == kBSkip) continue;
+          if (bcls(bi, 0) != kBZone && bcls(bi, 1) != kBZone) {
+            // A tie zone: this fold's ties split it, or it is one certain bucket.
+            const int E = bbin(bi, f);
+            const uint32_t D = readlane_u32(mD, zi);
+            uint32_t prev = 0;
+            if (cf == kBTie) {
+              if (!split_ready) {
+                lds_wait(&L.misc[kVSplitDone], kWaves - 1u, status);
+                split_ready = true;
+              }
+              const uint32_t t0 = readlane_u32(mT0, zi), tn = readlane_u32(mTn, zi);
+              for (uint32_t v = 0; v < tn && !fail; ++v) {
+                const uint32_t s = L.tord[t0 + v];
+                const uint32_t ab = L.tab[s];
+                if (!apply_units(E, ab - prev)) fail = true;
+                prev = ab;
+                const uint32_t q = L.tq[s];
+                const uint32_t par = (__float_as_uint(F) ^ q) & 1u;  // parity of M - q or M + q
+                if (!fail && !apply_units(E, (uint64_t)q + par)) fail = true;
+              }
+            }
+            if (!fail && !apply_units(E, D - prev)) fail = true;
+            if (!fail && !sp.sub && F >= sp.stop_ge) fail = true;
+            if (!fail && sp.sub && F < __uint_as_float(readlane_u32(mTub, zi))) fail = true;
+            continue;
+          }
+          const uint32_t base = readlane_u32(mBase, zi), n = readlane_u32(mN, zi), p0 = readlane_u32(mP0, zi);
+          if (cf == kBCert && !(bi & (kBStep << f)) && p0 + n <= pos_end) {
+            // Gathered for the other fold, certain for this one: one integer.
+            if (!apply_units(bbin(bi, f), readlane_u32(mD, zi))) fail = true;
+            else if (!sp.sub && F >= sp.stop_ge) fail = true;
+            else if (sp.sub && F < __uint_as_float(readlane_u32(mTub, zi))) fail = true;
+            if (!fail && p0 + n >= pos_end) at_keep = stopped = true;
+            continue;
+          }
+          uint32_t r0 = 0;
+          while (r0 < n && !stopped) {
+            const uint32_t r = r0 + lane;
+            float t = 0.0f;
+            uint32_t id = 0u;
+            if (r < n) {
+              const unsigned long long v = L.zpk[base + L.zperm[base + r]];
+              t = __uint_as_float((uint32_t)(v >> 32));
+              id = ~(uint32_t)v;
+            }
+            const bool live = r < n;
+            const bool past = live && p0 + r >= pos_end;
+            const uint32_t fb = __float_as_uint(F), ef = (fb >> 23) & 255u;
+            uint32_t done = 0u;  // lanes folded as integers before the one stepped in f32
+            if (F > 0.0f && ef >= 1u && ef <= 254u) {
+              const int E = (int)ef - 127;
+              const uint32_t M = (fb & 0x7fffffu) | 0x800000u;
+              bool tie = false, big = false;
+              const uint32_t q = live && !past ? rne_units(t, E, tie, big) : 0u;
+              const uint32_t incl = wave_incl_scan(q), excl = incl - q;
+              bool ev;
+              if (!sp.sub) {
+                const uint64_t Mi = (uint64_t)M + incl;
+                ev = tie || big || Mi >= (1ull << 24) || from_units((uint32_t)Mi, E) >= sp.stop_ge;
+              } else {
+                const bool ub = (uint64_t)excl + (1ull << 23) + 1ull > M;
+                const bool ui = (uint64_t)incl + (1ull << 23) + 1ull > M;
+                ev = tie || big || ub || ui || from_units(M - excl, E) < t;
+              }
+              ev = live && (ev || past);
+              const uint64_t m = __ballot(ev);
+              const uint32_t ev_lane = m ? (uint32_t)__ffsll((unsigned long long)m) - 1u : 64u;
+              done = min(ev_lane, n - r0);
+              if (done) {
+                const uint32_t sum = readlane_u32(incl, done - 1u);
+                const uint64_t M2 = sp.sub ? (uint64_t)M - sum : (uint64_t)M + sum;
+                F = from_units((uint32_t)M2, E);
+              }
+            }
+            if (r0 + done >= n) {
+              r0 = n;
+              break;
+            }
+            if (done == 64u) {  // no event in these 64
+              r0 += 64u;
+              continue;
+            }
+            // The event element (or the first one when F is not a normal number).
+            const uint32_t le = done;
+            const uint32_t pos = p0 + r0 + le;
+            if (pos >= pos_end) {
+              at_keep = stopped = true;  // the rest of the fold is outside it
+              break;
+            }
+            if (step(readlane_f32(t, le))) {
+              stop_pos = pos;
+              stop_id = readlane_u32(id, le);
+              stop_bk = k;
+              stopped = true;
+              break;
+            }
+            r0 += le + 1u;
+          }
+          // The walk ends with the zone that holds the cut (the last kept
+          // element), whatever certain buckets follow it.
+          if (!stopped && p0 + n >= pos_end) at_keep = stopped = true;
         }
       }
+      // Past the end without a stop, although a bucket was certain to lie
+      // past the stop: the approximation was wrong.
+      if (!fail && stop_pos == kNoPos && !at_keep && kb < kVB) fail = true;
+      res[f].F = F;
+      res[f].stop_pos = stop_pos;
+      res[f].stop_id = stop_id;
+      res[f].stop_bk = stop_bk;
+      if (f == 0) keep = stop_pos != kNoPos ? stop_pos + 1u : keep_count ? max(1u, L.misc[kVCount]) : keep_default;
     }
-    // Past the end without a stop, although a bucket was certain to lie
-    // past the stop: the approximation was wrong.
-    if (!fail && stop_pos == kNoPos && kb < kVB) fail = true;
     if (lane == 0) {
       L.misc[kVFail] = fail ? 1u : 0u;
-      L.misc[kVStopPos] = stop_pos;
-      L.misc[kVStopId] = stop_id;
-      L.misc[kVStopBk] = stop_bk;
-      L.misc[kVF] = __float_as_uint(F);
+      L.misc[kVKeep] = keep;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        L.misc[kVRes + 4 * f + 0] = __float_as_uint(res[f].F);
+        L.misc[kVRes + 4 * f + 1] = res[f].stop_pos;
+        L.misc[kVRes + 4 * f + 2] = res[f].stop_id;
+        L.misc[kVRes + 4 * f + 3] = res[f].stop_bk;
+      }
     }
   }
   __syncthreads();
-  res.F = __uint_as_float(L.misc[kVF]);
-  res.stop_pos = L.misc[kVStopPos];
-  res.stop_id = L.misc[kVStopId];
-  res.stop_bk = L.misc[kVStopBk];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    res[f].F = __uint_as_float(L.misc[kVRes + 4 * f + 0]);
+    res[f].stop_pos = L.misc[kVRes + 4 * f + 1];
+    res[f].stop_id = L.misc[kVRes + 4 * f + 2];
+    res[f].stop_bk = L.misc[kVRes + 4 * f + 3];
+  }
+  keep_out = L.misc[kVKeep];
   const bool ok = L.misc[kVFail] == 0u;
   __syncthreads();
   return ok;
@@ -824,10 +976,11 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   __syncthreads();
 
   // generate.rs:372-377: the softmax sum. The max element has x = 1, so S >= 1.
-  FoldRes r;
-  FoldSpec fs{0.0f, 0.0f, 0.0f, INFINITY, kVB, kVB, kNoPos, false};
-  if (!run_fold(fs, mx, L, src, r, a.status)) return false;
-  const float S = r.F;
+  FoldSpec fs[1] = {{0.0f, 0.0f, 0.0f, INFINITY, false}};
+  FoldRes r[1];
+  uint32_t keep;
+  if (!run_folds<1>(fs, mx, 0.0f, V, false, L, src, r, keep, a.status)) return false;
+  const float S = r[0].F;
   if (!(S > 0.0f) || !isfinite(S)) return false;
 
   // generate.rs:378-409: p = x / S; min-p by value (p is monotone along the
@@ -836,32 +989,19 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   const float p0 = 1.0f / S;
   const float thr = P.min_p > 0.0f ? P.min_p * p0 : 0.0f;
   auto cut_and_walk = [&](const auto& from) __attribute__((always_inline)) -> bool {
-    FoldSpec fc{0.0f, S, thr, P.top_p < 1.0f ? P.top_p : INFINITY, kVB, kVB, kNoPos, false};
-    FoldRes rc;
-    if (!run_fold(fc, mx, L, from, rc, a.status)) return false;
-    const bool cut = rc.stop_pos != kNoPos;
-    uint32_t keep;
-    if (cut) {
-      keep = rc.stop_pos + 1u;
-    } else if (P.min_p > 0.0f) {
-      keep = max(1u, L.misc[kVCount]);
-    } else {
-      keep = V;
-    }
     uint64_t st = a.rng_state[b];
     const float u = next_f32(st);
-    const float r0 = u * rc.F;
-    FoldSpec fw{r0, S, thr, INFINITY, cut ? rc.stop_bk + 1u : kVB, cut ? rc.stop_bk : kVB, keep, true};
-    FoldRes rw;
-    if (!run_fold(fw, mx, L, from, rw, a.status)) return false;
-    uint32_t pick;
-    if (rw.stop_pos != kNoPos) {
-      pick = rw.stop_id;
-    } else if (cut) {
-      pick = rc.stop_id;  // order[keep - 1]
-    } else {
-      return false;
-    }
+    FoldSpec fw[2] = {{0.0f, S, thr, P.top_p < 1.0f ? P.top_p : INFINITY, false},
+                      {0.0f, S, thr, INFINITY, true}};
+    FoldRes rw[2];
+    uint32_t keep;
+    if (!run_folds<2>(fw, mx, u, V, P.min_p > 0.0f, L, from, rw, keep, a.status)) return false;
+    // The walk's stop, else order[keep - 1] (the cut); without either the
+    // row is handed over.
+    const bool walk_stop = rw[1].stop_pos != kNoPos, cut = rw[0].stop_pos != kNoPos;
+    const uint32_t id_walk = rw[1].stop_id, id_cut = rw[0].stop_id;
+    if (!walk_stop && !cut) return false;
+    const uint32_t pick = walk_stop ? id_walk : id_cut;
     if (tid == 0) {
       store_result(a, b, pick, len_b);
       a.rng_state[b] = st;
