@@ -70,7 +70,8 @@ enum : uint32_t {
   kVSplitDone = 8,   // waves done with the tie split
   kVKeep = 9,        // the walk's end (sorted positions kept)
   kVRes = 10,        // fold results, 4 words per fold
-  kVMisc = 18,
+  kVTieMax = 18,     // last bucket holding a tie
+  kVMisc = 19,
 };
 
 struct VocabLds {
@@ -304,10 +305,13 @@ __device__ __forceinline__ bool before(uint32_t ka, uint32_t ia, uint32_t kb, ui
 // covers. The walk ends at sorted position keep (returned in keep_out): fold
 // 0's cut + 1, or without a cut the number of terms >= thr (at least 1) when
 // keep_count, else keep_default.
+//
+// tl lists every element of buckets 0 .. tl_k when tl_ok; a tie split whose
+// ties all lie in those buckets reads it instead of src.
 template <int NF, class Src>
 __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u, uint32_t keep_default, bool keep_count,
-                                          VocabLds& L, const Src& src, FoldRes (&res)[NF], uint32_t& keep_out,
-                                          uint32_t* status) {
+                                          VocabLds& L, const Src& src, const ListSrc& tl, bool tl_ok, uint32_t tl_k,
+                                          FoldRes (&res)[NF], uint32_t& keep_out, uint32_t* status) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t k0 = tid * 4u;
   const float S = fs[0].S, thr = fs[0].thr;  // the same terms for both folds
@@ -334,6 +338,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
     L.misc[kVNTies] = 0u;
     L.misc[kVCount] = 0u;
     L.misc[kVSplitDone] = 0u;
+    L.misc[kVTieMax] = 0u;
   }
 
   // Classification of this thread's 4 buckets from the approximate prefix.
@@ -594,6 +599,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
         r += (bu < bs || (bu == bs && before(L.tkey[v], L.tidx[v], ks, is))) ? 1u : 0u;
       }
       L.tord[r] = (uint16_t)s;
+      atomicMax(&L.misc[kVTieMax], bs & 0x7fffffffu);
       const uint32_t f = bs >> 31;
       atomicOr(&L.binfo[bs & 0x7fffffffu], (uint32_t)(kBTie ^ kBCert) << bcls_shift(f));  // CERT -> TIE
     }
@@ -603,12 +609,19 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
       L.segTub[s] = 0u;
     }
     __syncthreads();
+    // The buckets' state comes back from LDS (with the ties' classes), so
+    // none of it stays in registers across the exact pass.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t bi = L.binfo[k0 + j];
+      const uint32_t k = k0 + j;
+      const uint32_t bi = L.binfo[k];
+      c4[j] = L.cnt[k];
+      tub4[j] = term_of(glibc_expf_tab(-(float)k / kVR, L.exptab));
 #pragma unroll
-      for (int f = 0; f < NF; ++f)
-        if (bcls(bi, f) == kBTie) cl[f][j] = kBTie;
+      for (int f = 0; f < 2; ++f) {
+        cl[f][j] = (uint8_t)bcls(bi, f);
+        e4[f][j] = bbin(bi, f);
+      }
       carry4[j] = gathers(j) ? L.zcur[bslot(bi)] | (bi & (kBStep * 3u)) : 0u;
     }
     if (!layout()) return false;
@@ -636,11 +649,13 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
   }
 
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t bi = L.binfo[k0 + j];
+    const bool zone = bcls(bi, 0) >= kBZone || bcls(bi, 1) >= kBZone;  // gathered or split at ties
 #pragma unroll
     for (int f = 0; f < NF; ++f)
-      if (cl[f][j] == kBCert && !gathers(j) && !ties_in(j))
-        atomicAdd(&L.seg[f][bslot(L.binfo[k0 + j])], (unsigned long long)Df(f)[k0 + j]);
+      if (!zone && bcls(bi, f) == kBCert) atomicAdd(&L.seg[f][bslot(bi)], (unsigned long long)Df(f)[k0 + j]);
+  }
 
   // Sort each gathering zone by (key desc, id asc), ranking by counting
   // larger packed values; then replace each key by the element's term, so
@@ -668,10 +683,11 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
   __syncthreads();
 
   // Waves 1 .. 15 sum each tie bucket's ulp counts above each of its ties
-  // (a stream of the row) while wave 0 replays; wave 0 waits for them only
+  // (a stream of the row, or of the list when it covers every tie bucket)
+  // while wave 0 replays; wave 0 waits for them only
   // when it reaches the first tie zone.
   if (wave != 0 && nt) {
-    src.for_each_part([&](float w, uint32_t i) __attribute__((always_inline)) {
+    auto split = [&](float w, uint32_t i) __attribute__((always_inline)) {
       const float y = w - mx;
       const uint32_t k = vbucket(y);
       const uint32_t bi = L.binfo[k];
@@ -692,7 +708,9 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
           if (before(key, i, L.tkey[s], L.tidx[s])) atomicAdd(&L.tab[s], q);
         }
       }
-    }, 64u, kBlock - 64u);
+    };
+    if (tl_ok && L.misc[kVTieMax] <= tl_k) tl.for_each_part(split, 64u, kBlock - 64u);
+    else src.for_each_part(split, 64u, kBlock - 64u);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     if (lane == 0) atomicAdd(&L.misc[kVSplitDone], 1u);
   }
@@ -952,7 +970,8 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   unsigned long long* amass = L.zpk;
   for (uint32_t k = tid; k < kVB; k += kBlock) amass[k] = 0ull;
   // With min-p on, elements of the buckets that can reach p >= min_p * p_0
-  // (x >= ~min_p, so y >= ~ln(min_p); two buckets of slack) are listed.
+  // (x >= ~min_p, so y >= ~ln(min_p); two buckets of slack) are listed. The
+  // softmax sum's tie split reads the list too when every tie lies there.
   const uint32_t list_cap = (uint32_t)min((uint64_t)a.scratch_row_words / 2u, (uint64_t)kVListCap);
   const uint32_t kc = P.min_p > 0.0f && P.min_p <= 1.0f ? (uint32_t)fminf(-logf(P.min_p) * kVR + 2.0f, (float)(kVB - 1u)) : 0u;
   uint2* list = reinterpret_cast<uint2*>(a.scratch + (size_t)b * a.scratch_row_words);
@@ -976,10 +995,13 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   __syncthreads();
 
   // generate.rs:372-377: the softmax sum. The max element has x = 1, so S >= 1.
+  const uint32_t ncand = L.misc[kVCand];
+  const bool listed = kc && ncand <= list_cap;  // the list holds every element of buckets 0 .. kc
+  const ListSrc lsrc{list, listed ? ncand : 0u};
   FoldSpec fs[1] = {{0.0f, 0.0f, 0.0f, INFINITY, false}};
   FoldRes r[1];
   uint32_t keep;
-  if (!run_folds<1>(fs, mx, 0.0f, V, false, L, src, r, keep, a.status)) return false;
+  if (!run_folds<1>(fs, mx, 0.0f, V, false, L, src, lsrc, listed, kc, r, keep, a.status)) return false;
   const float S = r[0].F;
   if (!(S > 0.0f) || !isfinite(S)) return false;
 
@@ -995,7 +1017,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
                       {0.0f, S, thr, INFINITY, true}};
     FoldRes rw[2];
     uint32_t keep;
-    if (!run_folds<2>(fw, mx, u, V, P.min_p > 0.0f, L, from, rw, keep, a.status)) return false;
+    if (!run_folds<2>(fw, mx, u, V, P.min_p > 0.0f, L, from, lsrc, listed, kc, rw, keep, a.status)) return false;
     // The walk's stop, else order[keep - 1] (the cut); without either the
     // row is handed over.
     const bool walk_stop = rw[1].stop_pos != kNoPos, cut = rw[0].stop_pos != kNoPos;
@@ -1011,10 +1033,8 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   };
   // The list holds every element the two folds can include when the first
   // bucket past it lies wholly below the min-p threshold.
-  const uint32_t ncand = L.misc[kVCand];
-  if (kc && ncand <= list_cap && kc + 1u < kVB &&
-      glibc_expf_tab(-(float)(kc + 1u) / kVR, L.exptab) / S < thr) {
-    return cut_and_walk(ListSrc{list, ncand});
+  if (listed && kc + 1u < kVB && glibc_expf_tab(-(float)(kc + 1u) / kVR, L.exptab) / S < thr) {
+    return cut_and_walk(lsrc);
   }
   return cut_and_walk(src);
 }
