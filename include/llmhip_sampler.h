@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LLMHIP_ABI_VERSION 1
+#define LLMHIP_ABI_VERSION 2
 
 enum {
   LLMHIP_OK = 0,
@@ -166,6 +166,41 @@ int llmhip_decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
                        uint32_t* ring_len, uint32_t* done, size_t window, const uint8_t* allowed,
                        size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
                        void* stream);
+
+/*
+ * The allowed mask as bits, built on the device from a corpus's tokens
+ * (replaces Corpus::seen_tokens, crates/llm-core/src/corpus.rs:236-247,
+ * which generation passes as SamplingConfig::allowed on every call,
+ * crates/wasm-app/src/inference.rs:170). Bit id % 32 of word id / 32 of
+ * seen_bits is set when some tokens[i] == id; ids >= V are ignored, as
+ * seen.get_mut(id) ignores them. seen_bits has ceil(V / 32) words and is
+ * overwritten (the bits past V are cleared). tokens and seen_bits are
+ * device pointers; stream-ordered on `stream`. A corpus concatenates its
+ * sources' token lists into `tokens`; their order does not matter.
+ */
+int llmhip_seen_tokens(llmhip_ctx* ctx, const uint32_t* tokens, size_t n, size_t V, uint32_t* seen_bits,
+                       void* stream);
+
+/*
+ * llmhip_sample_device with the allowed mask as bits (as llmhip_seen_tokens
+ * writes them) instead of one byte per id: id < allowed_len is masked out
+ * when its bit is clear and id != eos_id (generate.rs:333-341, the same
+ * rule as the byte mask). A decode loop builds the mask once per
+ * generation and reads V / 8 bytes of it per call instead of V.
+ */
+int llmhip_sample_device_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                              const llmhip_params* params, size_t params_stride,
+                              const uint32_t* hist, const uint32_t* hist_offsets,
+                              const uint32_t* allowed_bits, size_t allowed_len, uint32_t eos_id,
+                              uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                              uint32_t* out_kept, void* stream);
+
+/* llmhip_decode_step with the allowed mask as bits (see above). */
+int llmhip_decode_step_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                            const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
+                            uint32_t* ring_len, uint32_t* done, size_t window, const uint32_t* allowed_bits,
+                            size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
+                            void* stream);
 
 #ifdef __cplusplus
 }

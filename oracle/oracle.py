@@ -108,3 +108,29 @@ def next_f32(state: int) -> tuple[float, int]:
     s = np.array([state], dtype=np.uint64)
     out = load().oracle_next_f32(_ptr(s))
     return float(out), int(s[0])
+
+
+def seen_tokens(tokens, V: int) -> np.ndarray:
+    """crates/llm-core/src/corpus.rs:236-247 (Corpus::seen_tokens): one flag per
+    id < V, set when some token equals it; ids >= V are skipped, as
+    seen.get_mut(id) returns None for them. `tokens` is the concatenation of
+    the corpus's token lists (the order does not matter)."""
+    seen = np.zeros(V, dtype=bool)
+    t = np.asarray(tokens, dtype=np.uint64).ravel()
+    seen[t[t < V].astype(np.int64)] = True
+    return seen
+
+
+def pack_bits(mask) -> np.ndarray:
+    """A bool mask as the C ABI's bit mask: bit i % 32 of u32 word i / 32."""
+    m = np.asarray(mask, dtype=bool).ravel()
+    words = (m.size + 31) // 32
+    padded = np.zeros(words * 32, dtype=bool)
+    padded[: m.size] = m
+    return np.packbits(padded, bitorder="little").view("<u4").astype(np.uint32)
+
+
+def unpack_bits(words, n: int) -> np.ndarray:
+    """Inverse of pack_bits for the first n ids."""
+    w = np.ascontiguousarray(words, dtype="<u4")
+    return np.unpackbits(w.view(np.uint8), bitorder="little")[:n].astype(bool)

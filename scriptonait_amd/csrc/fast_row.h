@@ -132,7 +132,9 @@ __device__ __forceinline__ float apply_penalty(float v, uint32_t m, float rp) {
 
 __device__ __forceinline__ bool masked_out(const SampleArgs& a, uint32_t id) {
   // generate.rs:333-341
-  return a.allowed && id < a.allowed_len && id != a.eos_id && a.allowed[id] == 0;
+  if (id >= a.allowed_len || id == a.eos_id) return false;
+  if (a.allowed) return a.allowed[id] == 0;
+  return a.allowed_bits && ((a.allowed_bits[id >> 5] >> (id & 31u)) & 1u) == 0u;
 }
 
 // Block-wide argmax of (bv, bi) pairs; every thread must call. Returns the

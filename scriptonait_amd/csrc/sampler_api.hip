@@ -16,6 +16,7 @@ hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s);
 hipError_t launch_general(const SampleArgs& a, hipStream_t s);
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
+hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s);
 }  // namespace llmhip
 
 using namespace llmhip;
@@ -99,7 +100,7 @@ struct Device {
 };
 
 int validate(size_t B, size_t V, size_t ld, const float* logits, const llmhip_params* params,
-             const uint32_t* hist, const uint32_t* hist_offsets, const uint8_t* allowed,
+             const uint32_t* hist, const uint32_t* hist_offsets, const void* allowed,
              size_t allowed_len, const uint64_t* rng_state, const uint32_t* out_ids) {
   if (B == 0) return LLMHIP_OK;
   if (!params) return arg_fail("params is null");
@@ -118,6 +119,13 @@ int validate(size_t B, size_t V, size_t ld, const float* logits, const llmhip_pa
 // `params_host` is read on the host to choose kernels; `params_dev` is its
 // device copy (null when params_stride == 0).
 // Decode-step mode (ring-buffer histories); ring == null for a CSR history.
+// The allowed mask: one byte per id or one bit per id (at most one is set).
+struct Mask {
+  const uint8_t* bytes = nullptr;
+  const uint32_t* bits = nullptr;
+  size_t len = 0;
+};
+
 struct RingArgs {
   uint32_t* ring = nullptr;
   uint32_t* ring_len = nullptr;
@@ -128,9 +136,9 @@ struct RingArgs {
 
 int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
             const llmhip_params* params_host, size_t params_stride, const llmhip_params* params_dev,
-            const uint32_t* hist, const uint32_t* hist_offsets, const uint8_t* allowed,
-            size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
-            float* out_probs, uint32_t* out_kept, hipStream_t s, const RingArgs& ring = RingArgs()) {
+            const uint32_t* hist, const uint32_t* hist_offsets, const Mask& mask, uint32_t eos_id,
+            uint64_t* rng_state, uint32_t* out_ids, float* out_probs, uint32_t* out_kept, hipStream_t s,
+            const RingArgs& ring = RingArgs()) {
   if (V == 0) {
     // Empty logits: sample_with returns 0 without drawing (generate.rs:375-377).
     HIP_TRY(hipMemsetAsync(out_ids, 0, B * sizeof(uint32_t), s));
@@ -172,8 +180,9 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.done = ring.done;
   a.ring_cap = ring.cap;
   a.window = ring.window;
-  a.allowed = allowed_len ? allowed : nullptr;
-  a.allowed_len = (uint32_t)allowed_len;
+  a.allowed = mask.len ? mask.bytes : nullptr;
+  a.allowed_bits = mask.len && !mask.bytes ? mask.bits : nullptr;
+  a.allowed_len = (uint32_t)mask.len;
   a.eos_id = eos_id;
   a.rng_state = rng_state;
   a.out_ids = out_ids;
@@ -189,7 +198,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   // last float4 must not extend past its V logits).
   const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0) && (V % 4 == 0);
   if (fast_mask) {
-    if (a.allowed) {
+    if (a.allowed || a.allowed_bits) {
       if ((st = ctx->slotmask.ensure(kBlock * sizeof(uint32_t)))) return st;
       HIP_TRY(launch_slotmask(a, static_cast<uint32_t*>(ctx->slotmask.ptr), s));
       a.slotmask = static_cast<const uint32_t*>(ctx->slotmask.ptr);
@@ -218,6 +227,37 @@ int copy_params(llmhip_ctx* ctx, const llmhip_params* params, size_t B, size_t p
   HIP_TRY(hipMemcpyAsync(ctx->params.ptr, params, bytes, hipMemcpyHostToDevice, s));
   *out_dev = static_cast<const llmhip_params*>(ctx->params.ptr);
   return LLMHIP_OK;
+}
+
+}  // namespace
+
+namespace {
+
+// One decode step (llmhip_decode_step and its bit-mask twin).
+int decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
+                uint32_t* ring_len, uint32_t* done, size_t window, const Mask& mask, const void* mask_ptr,
+                uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids, void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  int st = validate(B, V, ld, logits, params, nullptr, nullptr, mask_ptr, mask.len, rng_state, out_ids);
+  if (st || B == 0) return st;
+  if (!ring || !ring_len) return arg_fail("ring and ring_len are required");
+  if (ring_cap == 0 || ring_cap > 0x7fffffffu) return arg_fail("ring_cap must be in 1 .. 2^31-1");
+  if (window > ring_cap) return arg_fail("window must not exceed ring_cap");
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const llmhip_params* pdev = nullptr;
+  st = copy_params(ctx, params, B, params_stride, &pdev, s);
+  if (st) return st;
+  RingArgs r;
+  r.ring = ring;
+  r.ring_len = ring_len;
+  r.done = done;
+  r.cap = (uint32_t)ring_cap;
+  r.window = (uint32_t)window;
+  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, nullptr, nullptr, mask, eos_id, rng_state,
+                 out_ids, nullptr, nullptr, s, r);
 }
 
 }  // namespace
@@ -309,8 +349,47 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
   const llmhip_params* pdev = nullptr;
   st = copy_params(ctx, params, B, params_stride, &pdev, s);
   if (st) return st;
-  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, allowed,
-                 allowed_len, eos_id, rng_state, out_ids, out_probs, out_kept, s);
+  Mask m;
+  m.bytes = allowed;
+  m.len = allowed_len;
+  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state,
+                 out_ids, out_probs, out_kept, s);
+}
+
+int llmhip_sample_device_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                              const llmhip_params* params, size_t params_stride,
+                              const uint32_t* hist, const uint32_t* hist_offsets,
+                              const uint32_t* allowed_bits, size_t allowed_len, uint32_t eos_id,
+                              uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                              uint32_t* out_kept, void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  int st = validate(B, V, ld, logits, params, hist, hist_offsets, allowed_bits, allowed_len, rng_state,
+                    out_ids);
+  if (st || B == 0) return st;
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const llmhip_params* pdev = nullptr;
+  st = copy_params(ctx, params, B, params_stride, &pdev, s);
+  if (st) return st;
+  Mask m;
+  m.bits = allowed_bits;
+  m.len = allowed_len;
+  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state,
+                 out_ids, out_probs, out_kept, s);
+}
+
+int llmhip_seen_tokens(llmhip_ctx* ctx, const uint32_t* tokens, size_t n, size_t V, uint32_t* seen_bits,
+                       void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  if (V == 0) return LLMHIP_OK;
+  if (V > 0x7fffffffu) return arg_fail("V must be below 2^31");
+  if (!seen_bits) return arg_fail("seen_bits is null");
+  if (n > 0 && !tokens) return arg_fail("tokens is null but n > 0");
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  HIP_TRY(launch_seen_bits(tokens, n, (uint32_t)V, seen_bits, static_cast<hipStream_t>(stream)));
+  return LLMHIP_OK;
 }
 
 int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
@@ -362,10 +441,12 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
   const llmhip_params* pdev = nullptr;
   if ((st = copy_params(ctx, params, B, params_stride, &pdev, s))) return st;
 
+  Mask m;
+  m.bytes = allowed_len ? static_cast<const uint8_t*>(ctx->allowed.ptr) : nullptr;
+  m.len = allowed_len;
   st = enqueue(ctx, dlog, B, V, V, params, params_stride, pdev,
                hist ? static_cast<const uint32_t*>(ctx->hist.ptr) : nullptr,
-               hist ? static_cast<const uint32_t*>(ctx->hoff.ptr) : nullptr,
-               allowed_len ? static_cast<const uint8_t*>(ctx->allowed.ptr) : nullptr, allowed_len,
+               hist ? static_cast<const uint32_t*>(ctx->hoff.ptr) : nullptr, m,
                eos_id, static_cast<uint64_t*>(ctx->rng.ptr), static_cast<uint32_t*>(ctx->ids.ptr),
                out_probs ? static_cast<float*>(ctx->probs.ptr) : nullptr,
                out_kept ? static_cast<uint32_t*>(ctx->kept.ptr) : nullptr, s);
@@ -395,26 +476,23 @@ int llmhip_decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
                        uint32_t* ring_len, uint32_t* done, size_t window, const uint8_t* allowed,
                        size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
                        void* stream) {
-  if (!ctx) return arg_fail("ctx is null");
-  int st = validate(B, V, ld, logits, params, nullptr, nullptr, allowed, allowed_len, rng_state, out_ids);
-  if (st || B == 0) return st;
-  if (!ring || !ring_len) return arg_fail("ring and ring_len are required");
-  if (ring_cap == 0 || ring_cap > 0x7fffffffu) return arg_fail("ring_cap must be in 1 .. 2^31-1");
-  if (window > ring_cap) return arg_fail("window must not exceed ring_cap");
-  Device d(ctx->device);
-  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const llmhip_params* pdev = nullptr;
-  st = copy_params(ctx, params, B, params_stride, &pdev, s);
-  if (st) return st;
-  RingArgs r;
-  r.ring = ring;
-  r.ring_len = ring_len;
-  r.done = done;
-  r.cap = (uint32_t)ring_cap;
-  r.window = (uint32_t)window;
-  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, nullptr, nullptr, allowed, allowed_len,
-                 eos_id, rng_state, out_ids, nullptr, nullptr, s, r);
+  Mask m;
+  m.bytes = allowed;
+  m.len = allowed_len;
+  return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, window, m,
+                     allowed, eos_id, rng_state, out_ids, stream);
+}
+
+int llmhip_decode_step_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                            const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
+                            uint32_t* ring_len, uint32_t* done, size_t window, const uint32_t* allowed_bits,
+                            size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
+                            void* stream) {
+  Mask m;
+  m.bits = allowed_bits;
+  m.len = allowed_len;
+  return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, window, m,
+                     allowed_bits, eos_id, rng_state, out_ids, stream);
 }
 
 }  // extern "C"

@@ -53,11 +53,15 @@ struct SampleArgs {
   llmhip_params shared;          // used when params == null
   const uint32_t* hist;          // device, may be null
   const uint32_t* hist_offsets;  // device [B+1], may be null
+  // The allowed mask (generate.rs:333-341) covers ids < allowed_len, as one
+  // byte per id (allowed) or one bit per id (allowed_bits: bit id % 32 of
+  // word id / 32 set = allowed); at most one of the two is set.
   const uint8_t* allowed;        // device, may be null
+  const uint32_t* allowed_bits;  // device, may be null
   uint32_t allowed_len;
   // Fast path: bit e of word t is set when thread t's slot e is masked out
-  // by `allowed` (the fast kernel's layout, built by a prep kernel), or all
-  // zeros when there is no mask. 1024 words, always valid.
+  // by the allowed mask (the fast kernel's layout, built by a prep kernel),
+  // or all zeros when there is no mask. 1024 words, always valid.
   const uint32_t* slotmask;
   // Decode-step mode (ring_cap > 0): row b's history is the last
   // min(ring_len[b], window) tokens of the ring ring[b*ring_cap ..

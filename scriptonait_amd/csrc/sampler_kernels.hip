@@ -12,6 +12,8 @@
 //    V, and rows the fast kernel cannot bound): a stable LSD radix sort of
 //    (key, id) pairs in per-row HBM scratch gives exactly the reference's
 //    `order`, followed by the same sequential tail.
+#include <algorithm>
+
 #include "draw_tail.h"
 #include "fast_row.h"
 #include "sampler_common.h"
@@ -221,6 +223,46 @@ __global__ __launch_bounds__(kBlock) void slotmask_kernel(SampleArgs a, uint32_t
 }
 
 // ---------------------------------------------------------------------------
+// Allowed mask as bits from a corpus's tokens (Corpus::seen_tokens,
+// crates/llm-core/src/corpus.rs:236-247): bit id is set when some token
+// equals id < V; larger ids are ignored, as seen.get_mut(id) ignores them.
+// Each workgroup ORs its share of the tokens into an LDS copy of the mask
+// (repeated ids then cost LDS atomics, not global ones) and merges the
+// nonzero words into the output, which a fill kernel has cleared. Masks
+// larger than the LDS copy are set with global atomics directly.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kSeenLdsWords = 16384;  // 64 KiB: masks of V <= 2^19 ids go through LDS
+constexpr uint32_t kSeenMaxBlocks = 512;
+
+__global__ __launch_bounds__(kBlock) void fill_u32_kernel(uint32_t* p, uint32_t n, uint32_t v) {
+  for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) p[i] = v;
+}
+
+__global__ __launch_bounds__(kBlock) void seen_bits_kernel(const uint32_t* tokens, uint64_t n, uint32_t V,
+                                                           uint32_t* bits) {
+  __shared__ uint32_t m[kSeenLdsWords];
+  const uint32_t words = (V + 31u) / 32u;
+  const bool lds = words <= kSeenLdsWords;
+  if (lds) {
+    for (uint32_t i = threadIdx.x; i < words; i += kBlock) m[i] = 0u;
+    __syncthreads();
+  }
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const uint32_t id = tokens[i];
+    if (id < V) {
+      if (lds) atomicOr(&m[id >> 5], 1u << (id & 31u));
+      else atomicOr(&bits[id >> 5], 1u << (id & 31u));
+    }
+  }
+  if (lds) {
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < words; i += kBlock)
+      if (m[i]) atomicOr(&bits[i], m[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side launch.
 // ---------------------------------------------------------------------------
 template <int NCH>
@@ -254,6 +296,18 @@ hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s) {
 
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(sample_vocab_kernel, dim3(a.B), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s) {
+  const uint32_t words = (V + 31u) / 32u;
+  const uint32_t fb = (uint32_t)std::min<uint64_t>((words + kBlock - 1u) / kBlock, 1024u);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(fb), dim3(kBlock), 0, s, bits, words, 0u);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || n == 0) return e;
+  const uint64_t per = words <= kSeenLdsWords ? 16u * kBlock : (uint64_t)kBlock;  // tokens per block and pass
+  const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + per - 1u) / per, kSeenMaxBlocks);
+  hipLaunchKernelGGL(seen_bits_kernel, dim3(blocks), dim3(kBlock), 0, s, tokens, n, V, bits);
   return hipGetLastError();
 }
 

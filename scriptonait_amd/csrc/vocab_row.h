@@ -1108,12 +1108,16 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   // Each test on a row-wide condition is a branch of its own, so rows with
   // no mask, no penalty or T == 1 pay nothing per element for it.
   const uint8_t* allowed = a.allowed;
+  const uint32_t* allowed_bits = a.allowed_bits;
   const uint32_t allowed_len = a.allowed_len, eos = a.eos_id;
   const bool div_t = T != 1.0f;
-  auto wval = [allowed, allowed_len, eos, &L, use_pen, div_t, T](uint32_t i, float v)
+  auto wval = [allowed, allowed_bits, allowed_len, eos, &L, use_pen, div_t, T](uint32_t i, float v)
       __attribute__((always_inline)) -> float {
     if (allowed) {  // generate.rs:333-341
       if (i < allowed_len && i != eos && allowed[i] == 0) v = -INFINITY;
+    }
+    if (allowed_bits) {
+      if (i < allowed_len && i != eos && ((allowed_bits[i >> 5] >> (i & 31u)) & 1u) == 0u) v = -INFINITY;
     }
     if (use_pen) {
       if ((L.hbits[(i >> 5) & (kVBits - 1u)] >> (i & 31u)) & 1u) {

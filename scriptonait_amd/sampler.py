@@ -43,6 +43,9 @@ EXPORTED_SYMBOLS = (
     "llmhip_sample_host",
     "llmhip_sample_device",
     "llmhip_decode_step",
+    "llmhip_seen_tokens",
+    "llmhip_sample_device_bits",
+    "llmhip_decode_step_bits",
 )
 
 
@@ -91,6 +94,12 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.llmhip_sample_device.argtypes = common + [vp]
     lib.llmhip_decode_step.restype = ctypes.c_int
     lib.llmhip_decode_step.argtypes = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, sz, vp, sz, u32, vp, vp, vp]
+    lib.llmhip_sample_device_bits.restype = ctypes.c_int
+    lib.llmhip_sample_device_bits.argtypes = common + [vp]
+    lib.llmhip_decode_step_bits.restype = ctypes.c_int
+    lib.llmhip_decode_step_bits.argtypes = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, sz, vp, sz, u32, vp, vp, vp]
+    lib.llmhip_seen_tokens.restype = ctypes.c_int
+    lib.llmhip_seen_tokens.argtypes = [vp, vp, sz, sz, vp, vp]
     _lib = lib
     return lib
 
@@ -231,10 +240,13 @@ class Sampler:
 
     def sample_device(self, logits, params: np.ndarray, rng_state, out_ids, V: Optional[int] = None,
                       hist=None, hist_offsets=None, allowed=None, eos_id: int = EOS,
-                      out_probs=None, out_kept=None, stream=None) -> None:
+                      out_probs=None, out_kept=None, stream=None, allowed_bits=None,
+                      allowed_len: Optional[int] = None) -> None:
         """llmhip_sample_device on torch CUDA tensors (logits [B, ld] f32,
         rng_state [B] int64 viewed as u64, out_ids [B] int32). Enqueued on
-        `stream` (default: torch's current stream); does not synchronize."""
+        `stream` (default: torch's current stream); does not synchronize.
+        With allowed_bits (int32 words, as seen_tokens writes them; covering
+        allowed_len ids, default V) it calls llmhip_sample_device_bits."""
         import torch
 
         B, ld = logits.shape
@@ -244,16 +256,41 @@ class Sampler:
         if stream is None:
             stream = torch.cuda.current_stream(logits.device)
         dp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-        status = self.lib.llmhip_sample_device(
-            self.ctx, dp(logits), B, V, ld, _ptr(params), stride,
-            dp(hist), dp(hist_offsets), dp(allowed),
-            0 if allowed is None else allowed.numel(), eos_id,
-            dp(rng_state), dp(out_ids), dp(out_probs), dp(out_kept), stream.cuda_stream)
+        if allowed_bits is not None:
+            if allowed is not None:
+                raise ValueError("pass allowed or allowed_bits, not both")
+            status = self.lib.llmhip_sample_device_bits(
+                self.ctx, dp(logits), B, V, ld, _ptr(params), stride,
+                dp(hist), dp(hist_offsets), dp(allowed_bits), V if allowed_len is None else allowed_len,
+                eos_id, dp(rng_state), dp(out_ids), dp(out_probs), dp(out_kept), stream.cuda_stream)
+        else:
+            status = self.lib.llmhip_sample_device(
+                self.ctx, dp(logits), B, V, ld, _ptr(params), stride,
+                dp(hist), dp(hist_offsets), dp(allowed),
+                0 if allowed is None else allowed.numel(), eos_id,
+                dp(rng_state), dp(out_ids), dp(out_probs), dp(out_kept), stream.cuda_stream)
         _check(self.lib, status)
+
+    def seen_tokens(self, tokens, V: int, out_bits=None, stream=None):
+        """llmhip_seen_tokens: the allowed mask as bits (an int32 CUDA tensor
+        of ceil(V / 32) words) from a CUDA tensor of token ids (int32 viewed
+        as u32). Enqueued on `stream` (default: torch's current stream)."""
+        import torch
+
+        words = (V + 31) // 32
+        if out_bits is None:
+            out_bits = torch.empty(max(words, 1), dtype=torch.int32, device=tokens.device)
+        if stream is None:
+            stream = torch.cuda.current_stream(tokens.device)
+        status = self.lib.llmhip_seen_tokens(self.ctx, tokens.data_ptr() if tokens.numel() else None,
+                                             tokens.numel(), V, out_bits.data_ptr(), stream.cuda_stream)
+        _check(self.lib, status)
+        return out_bits
 
 
     def decode_step(self, logits, params: np.ndarray, ring, ring_len, done, window: int, rng_state, out_ids,
-                    V: Optional[int] = None, allowed=None, eos_id: int = EOS, stream=None) -> None:
+                    V: Optional[int] = None, allowed=None, eos_id: int = EOS, stream=None, allowed_bits=None,
+                    allowed_len: Optional[int] = None) -> None:
         """llmhip_decode_step on torch CUDA tensors: one Generator::step
         (generate.rs:157-165) for B generations whose history ring
         ([B, ring_cap] int32), lengths and done flags ([B] int32) and RNG
@@ -268,10 +305,18 @@ class Sampler:
         if stream is None:
             stream = torch.cuda.current_stream(logits.device)
         dp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-        status = self.lib.llmhip_decode_step(
-            self.ctx, dp(logits), B, V, ld, _ptr(params), stride, dp(ring), ring.shape[1], dp(ring_len),
-            dp(done), window, dp(allowed), 0 if allowed is None else allowed.numel(), eos_id,
-            dp(rng_state), dp(out_ids), stream.cuda_stream)
+        if allowed_bits is not None:
+            if allowed is not None:
+                raise ValueError("pass allowed or allowed_bits, not both")
+            status = self.lib.llmhip_decode_step_bits(
+                self.ctx, dp(logits), B, V, ld, _ptr(params), stride, dp(ring), ring.shape[1], dp(ring_len),
+                dp(done), window, dp(allowed_bits), V if allowed_len is None else allowed_len, eos_id,
+                dp(rng_state), dp(out_ids), stream.cuda_stream)
+        else:
+            status = self.lib.llmhip_decode_step(
+                self.ctx, dp(logits), B, V, ld, _ptr(params), stride, dp(ring), ring.shape[1], dp(ring_len),
+                dp(done), window, dp(allowed), 0 if allowed is None else allowed.numel(), eos_id,
+                dp(rng_state), dp(out_ids), stream.cuda_stream)
         _check(self.lib, status)
 
 
