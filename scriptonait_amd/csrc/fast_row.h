@@ -15,15 +15,15 @@
 //
 // Per wave:
 //  1. the row lands: per-chunk and per-thread maxima.
-//  2. the first 12 waves to get here put their per-thread maxima in a
-//     two-level key histogram; the 12th selects the threshold (about 1.5K
-//     of the row's values expected at or above it, scaled from the 3/4 of
-//     the row those waves hold) and publishes it in LDS.
-//  3. each chunk whose maximum reaches the threshold is compared value by
+//  2. the first kTauWaves (8) waves to get here put their per-thread maxima
+//     in a two-level key histogram; the 8th selects the threshold (about
+//     1.6K of the row's values expected at or above it, scaled from the half
+//     of the row those waves hold) and publishes it in LDS.
+//  3. the same 8 waves count the history ids: u16 multiplicities and
+//     per-owner masks of penalized slots, integer LDS atomics whose result
+//     does not depend on order.
+//  4. each chunk whose maximum reaches the threshold is compared value by
 //     value; hits go to the wave's LDS region.
-//  4. history ids are counted: u16 multiplicities and per-owner masks of
-//     penalized slots, integer LDS atomics whose result does not depend on
-//     order.
 //  5. the wave settles its hits (mask, penalty m times in sequence,
 //     recheck, one division by T) into the candidate list.
 //  6. barrier; the count check (>= K proves the threshold); rank; barrier.
@@ -65,7 +65,6 @@ struct GenLds {
 
 constexpr uint32_t kFastCand = 2048;              // candidates per row
 constexpr uint32_t kEntries = 64;                 // scan entries per wave
-constexpr uint32_t kHistPerThread = 1;            // history ids fetched per thread with the row
 constexpr uint32_t kCoarseBins = 256;             // key bits 31..24
 constexpr uint32_t kFineBins = 4096;              // key bits 31..20
 constexpr uint32_t kTauWaves = 8;                 // waves whose maxima form the threshold sample
@@ -76,8 +75,7 @@ constexpr int kSyncSample = 0;  // waves whose sample is in the histogram
 constexpr int kSyncHist = 1;    // waves whose history ids are counted
 constexpr int kCandN = 2;       // candidates in ord[]
 constexpr int kOverflow = 3;    // some wave's region overflowed
-constexpr int kTauState = 4;    // 0: not yet, 1: published in kTauKey, 2: row not bounded here
-constexpr int kTauKey = 5;
+constexpr int kTauState = 4;    // 0: not yet, 1: row not bounded here, else the threshold key
 constexpr int kArrive = 6;   // waves whose row has landed, in arrival order
 constexpr int kSampled = 7;  // row positions held by the sample waves
 constexpr int kSyncZero = 8; // waves whose share of the count table is zeroed
@@ -193,6 +191,21 @@ __device__ __forceinline__ void lds_wait(const uint32_t* ctr, uint32_t target, u
     __builtin_amdgcn_s_sleep(1);
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Wait until *p != 0 and return that value (0 if the bounded spin ran out,
+// as in lds_wait).
+__device__ __forceinline__ uint32_t lds_wait_nonzero(const uint32_t* p, uint32_t* status) {
+  uint32_t spins = 0, v;
+  while ((v = lds_peek(p)) == 0u) {
+    if (++spins > kSpinLimit) {
+      if ((threadIdx.x & 63u) == 0u) atomicOr(status, kStatusSyncTimeout);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  return v;
 }
 
 #ifndef LLMHIP_STRIDED
@@ -397,8 +410,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // limited rate (a CU holds only part of its 128 KiB row in flight, and a
   // wave stalls at a load until earlier data has returned), so every wave
   // issues its part of the row as early as it can: the first two chunks,
-  // the LDS set-up and its barrier in their shadow, then the rest, then the
-  // history ids (their offsets are back by then).
+  // the LDS set-up and its barrier in their shadow, then the rest. The
+  // history ids are fetched later, by the first waves whose rows are in.
   //
   // The row's scalars go out first, by vector loads (lane l reads word l),
   // which count in order with the row's loads: a scalar load would share its
@@ -464,15 +477,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   const HistRow hr = hist_row(a, b, h0, h1);
   const uint32_t H = rp != 1.0f ? hr.H : 0u;
   const bool use_pen = H > 0 && H < 65536u;
-  // History ids: lane t of the workgroup fetches ids t, t+1024, ...; they
-  // land right behind the wave's part of the row.
-  uint32_t hid[kHistPerThread];
-  {
-    const uint32_t hmax = use_pen ? H - 1u : 0u;
-#pragma unroll
-    for (uint32_t u = 0; u < kHistPerThread; ++u) hid[u] = use_pen ? hr.at(min(tid + u * kBlock, hmax)) : a.slotmask[0];
-  }
-  __builtin_amdgcn_sched_barrier(0);
   // This wave's share of the count table (only when a history may be used).
   if (a.hist) {
     uint4* c4 = reinterpret_cast<uint4*>(L.cnt);
@@ -523,14 +527,22 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   };
   // History multiplicities (integer LDS atomics: the counts do not depend on
   // the order). The first occurrence of an id marks its slot in the owner
-  // thread's mask.
-  auto count_history = [&]() __attribute__((always_inline)) {
+  // thread's mask. Waves part = 0 .. nparts-1 share the ids, 8 per lane in
+  // flight at a time.
+  auto count_history = [&](uint32_t part, uint32_t nparts) __attribute__((always_inline)) {
     if (use_pen) {
       lds_wait(&L.misc[kSyncZero], kWaves, a.status);
+      const uint32_t stride = nparts * 64u;
+      for (uint32_t j0 = part * 64u; j0 < H; j0 += 8u * stride) {
+        uint32_t ids[8];
 #pragma unroll
-      for (uint32_t u = 0; u < kHistPerThread; ++u)
-        if (tid + u * kBlock < H) add_hist(hid[u]);
-      for (uint32_t j = tid + kHistPerThread * kBlock; j < H; j += kBlock) add_hist(hr.at(j));
+        for (uint32_t u = 0; u < 8u; ++u) {
+          const uint32_t j = j0 + u * stride + lane;
+          ids[u] = j < H ? hr.at(j) : 0xffffffffu;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 8u; ++u) add_hist(ids[u]);  // ids >= V are ignored
+      }
     }
     lds_signal(&L.misc[kSyncHist]);
   };
@@ -554,7 +566,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     // ops/loss.rs:6-16 over the masked, penalized row (before temperature).
 #pragma unroll
     for (int c = 0; c < NCH; ++c) prep(c);
-    count_history();
+    count_history(wave, kWaves);
     uint32_t pmv = 0u;
     if (use_pen) {
       lds_wait(&L.misc[kSyncHist], kWaves, a.status);
@@ -597,10 +609,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   //    histogram, and the last of them selects the speculative threshold:
   //    the Q-th largest sampled maximum, with Q scaled from the target
   //    (kSpecNum/kSpecDen)*K to the positions the sample holds.
+  uint32_t arrive = 0u;
+  if (lane == 0u) arrive = __hip_atomic_fetch_add(&L.misc[kArrive], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  arrive = readlane_u32(arrive, 0);
   {
-    uint32_t arrive = 0u;
-    if (lane == 0u) arrive = __hip_atomic_fetch_add(&L.misc[kArrive], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    arrive = readlane_u32(arrive, 0);
     if (arrive < kTauWaves) {
       if (tm > -INFINITY) {  // a NaN or -inf maximum is not counted
         const uint32_t k = f2key(tm);
@@ -615,25 +627,24 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
         const uint32_t Q =
             (uint32_t)(((uint64_t)kSpecNum * K * sampled + (uint64_t)kSpecDen * V - 1u) / ((uint64_t)kSpecDen * V)) + 2u;
         const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, Q, false, lane), T, lane);
-        if (lane == 0) {
-          L.misc[kTauKey] = tkey;
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-          __hip_atomic_store(&L.misc[kTauState], tkey ? 1u : 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
+        // A bounded threshold key is above 0x007fffff (lower_past_ties), so
+        // 1 is free to say "not bounded".
+        if (lane == 0) __hip_atomic_store(&L.misc[kTauState], tkey ? tkey : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
     }
   }
-  // The history counts (the ids land right behind the wave's chunks).
-  count_history();
+  // The history counts, by the same first kTauWaves waves: their ids are
+  // fetched while the other waves' rows are still landing, so the waves
+  // whose rows land last find the counts done.
+  if (arrive < kTauWaves) count_history(arrive, kTauWaves);
 
   // 3. The scan: every lane whose maximum over a chunk reaches the
   //    published threshold appends one entry (the chunk's 4 values and its
   //    position) to the wave's region: one compare per chunk, and for the
   //    chunks where some lane hits, one ballot offset and two LDS writes.
-  lds_wait(&L.misc[kTauState], 1u, a.status);
-  const uint32_t tau = lds_peek(&L.misc[kTauState]);
-  if (tau != 1u) return false;  // every wave read the same published state
-  float tf = key2f(L.misc[kTauKey]);
+  const uint32_t tau = lds_wait_nonzero(&L.misc[kTauState], a.status);
+  if (tau <= 1u) return false;  // every wave read the same published state
+  float tf = key2f(tau);
   LLMHIP_MARK(4);
   uint32_t nent = 0u;  // this wave's entries
   auto scan_chunk = [&](int c, float mcv) __attribute__((always_inline)) {
@@ -702,7 +713,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
   };
   if (use_pen) {
-    lds_wait(&L.misc[kSyncHist], kWaves, a.status);
+    lds_wait(&L.misc[kSyncHist], kTauWaves, a.status);
     pmv = L.pm[tid];
   }
   settle(false);
