@@ -171,7 +171,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
     }
   }
   // generate.rs:375-377: degenerate exit, no draw.
-  if (!(sum > 0.0f) || !isfinite(sum)) {
+  if (__builtin_expect(!(sum > 0.0f) || !isfinite(sum), 0)) {
     if (lane == 0) {
       store_result(a, b, n > 0 ? my_id : 0u, len_b);
       if (a.out_kept) a.out_kept[b] = 0u;
@@ -239,7 +239,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
     }
   }
 
-  if (!cert) {
+  if (__builtin_expect(!cert, 0)) {
     buf[lane] = p;
     // Terms 8k .. 8k+7, read from LDS per block (broadcast).
     auto block = [&](int kk, float (&t8)[8]) __attribute__((always_inline)) {

@@ -508,7 +508,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
     return true;
   }
-  if (H >= 65536u) return false;  // a u16 multiplicity could overflow
+  if (__builtin_expect(H >= 65536u, 0)) return false;  // a u16 multiplicity could overflow
   const bool greedy = cls == kClassGreedy;
   // A penalty below 1 (or NaN) can raise a value above the raw one, so the
   // selection on raw values below does not bound such rows.
@@ -562,7 +562,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
   };
 
-  if (greedy) {
+  if (__builtin_expect(greedy, 0)) {
     // ops/loss.rs:6-16 over the masked, penalized row (before temperature).
 #pragma unroll
     for (int c = 0; c < NCH; ++c) prep(c);
@@ -670,7 +670,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   //    atomic per round.
   uint32_t pmv = 0u;
   auto settle = [&](bool final) __attribute__((always_inline)) {
-    if (nent > kEntries) {
+    if (__builtin_expect(nent > kEntries, 0)) {
       if (lane == 0) atomicOr(&L.misc[kOverflow], 1u);
       return;
     }
@@ -721,7 +721,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   LLMHIP_MARK(6);
   uint32_t n = L.misc[kCandN];
   LLMHIP_NOTE(12, n);
-  if (n < K || n > kFastCand || L.misc[kOverflow]) {
+  if (__builtin_expect(n < K || n > kFastCand || L.misc[kOverflow], 0)) {
     LLMHIP_NOTE(13, 1);
     // The speculative threshold failed: use the exact one, the lower edge of
     // the fine bin holding the K-th largest of the 1024 per-thread maxima of
@@ -778,7 +778,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
 
   // 7. The sequential tail (one wave).
   if (wave == 0) {
-    if (K <= 64) {
+    if (__builtin_expect(K <= 64, 1)) {
       draw_tail_bcast(a, b, len_b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u,
                       u_draw, st_next, L.exptab, L.tail);
     } else {

@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
 template <int NCH, bool VEC>
 __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   __shared__ FastLds<NCH> L;
-  if (!fast_row<NCH, VEC>(a, L)) {
+  if (__builtin_expect(!fast_row<NCH, VEC>(a, L), 0)) {
     __syncthreads();
     general_row(a, blockIdx.x, L.gen);
   }
