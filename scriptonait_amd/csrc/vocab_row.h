@@ -71,7 +71,9 @@ enum : uint32_t {
   kVKeep = 9,        // the walk's end (sorted positions kept)
   kVRes = 10,        // fold results, 4 words per fold
   kVTieMax = 18,     // last bucket holding a tie
-  kVMisc = 19,
+  kVSortDone = 19,   // waves done with their share of the zone sort
+  kVSplitNext = 20,  // next block of the tie split to claim
+  kVMisc = 21,
 };
 
 struct VocabLds {
@@ -240,6 +242,42 @@ struct StreamSrc {
   __device__ __forceinline__ void for_each(F&& f) const {
     for_each_part(f, 0u, kBlock);
   }
+  // Elements blk * 1024 .. blk * 1024 + 1023, by the calling wave.
+  __device__ __forceinline__ uint32_t blocks() const { return (V + 1023u) / 1024u; }
+  template <class F>
+  __device__ __forceinline__ void for_each_block(F&& f, uint32_t blk) const {
+    const uint32_t lane = threadIdx.x & 63u;
+    if (vec4) {
+      const float4* r4 = reinterpret_cast<const float4*>(row);
+      const uint32_t nq = (V + 3u) / 4u;
+      float4 v4[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t q = blk * 256u + lane + 64u * s;
+        v4[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t i = 4u * (blk * 256u + lane + 64u * s);
+        const float v[4] = {v4[s].x, v4[s].y, v4[s].z, v4[s].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (i + c < V) f(wval(i + c, v[c]), i + c);
+      }
+    } else {
+      float v[16];
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const uint32_t i = blk * 1024u + lane + 64u * s;
+        v[s] = i < V ? row[i] : 0.0f;
+      }
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const uint32_t i = blk * 1024u + lane + 64u * s;
+        if (i < V) f(wval(i, v[s]), i);
+      }
+    }
+  }
 };
 
 // The min-p candidates of a row, listed by the histogram pass as (key, id)
@@ -258,6 +296,20 @@ struct ListSrc {
   template <class F>
   __device__ __forceinline__ void for_each(F&& f) const {
     for_each_part(f, 0u, kBlock);
+  }
+  __device__ __forceinline__ uint32_t blocks() const { return (n + 1023u) / 1024u; }
+  template <class F>
+  __device__ __forceinline__ void for_each_block(F&& f, uint32_t blk) const {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint2 e[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const uint32_t j = blk * 1024u + lane + 64u * s;
+      e[s] = j < n ? list[j] : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      if (blk * 1024u + lane + 64u * s < n) f(key2f(e[s].x), e[s].y);
   }
 };
 
@@ -339,6 +391,8 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
     L.misc[kVCount] = 0u;
     L.misc[kVSplitDone] = 0u;
     L.misc[kVTieMax] = 0u;
+    L.misc[kVSortDone] = 0u;
+    L.misc[kVSplitNext] = 0u;
   }
 
   // Classification of this thread's 4 buckets from the approximate prefix.
@@ -680,12 +734,13 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
       L.zpk[base + i] = ((unsigned long long)__float_as_uint(t) << 32) | (uint32_t)v;
     }
   }
-  __syncthreads();
+  lds_signal(&L.misc[kVSortDone]);
 
-  // Waves 1 .. 15 sum each tie bucket's ulp counts above each of its ties
-  // (a stream of the row, or of the list when it covers every tie bucket)
-  // while wave 0 replays; wave 0 waits for them only
-  // when it reaches the first tie zone.
+  // Waves 1 .. 15, each as soon as its share of the sort is done, sum each
+  // tie bucket's ulp counts above each of its ties: they claim blocks of the
+  // row (or of the list, when it covers every tie bucket) one at a time, so
+  // the re-read overlaps the sort of the largest zones and wave 0's replay.
+  // Wave 0 waits for them only when it reaches the first tie zone.
   if (wave != 0 && nt) {
     auto split = [&](float w, uint32_t i) __attribute__((always_inline)) {
       const float y = w - mx;
@@ -709,16 +764,24 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
         }
       }
     };
-    if (tl_ok && L.misc[kVTieMax] <= tl_k) tl.for_each_part(split, 64u, kBlock - 64u);
-    else src.for_each_part(split, 64u, kBlock - 64u);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    if (lane == 0) atomicAdd(&L.misc[kVSplitDone], 1u);
+    const bool from_list = tl_ok && L.misc[kVTieMax] <= tl_k;
+    const uint32_t nb = from_list ? tl.blocks() : src.blocks();
+    for (;;) {
+      uint32_t blk = 0u;
+      if (lane == 0) blk = atomicAdd(&L.misc[kVSplitNext], 1u);
+      blk = readlane_u32(blk, 0);
+      if (blk >= nb) break;
+      if (from_list) tl.for_each_block(split, blk);
+      else src.for_each_block(split, blk);
+    }
+    lds_signal(&L.misc[kVSplitDone]);
   }
 
   // Replays (wave 0), one fold after the other: certain segments as
   // integers, tie zones split at their ties, gathering zones 64 elements at a
   // time.
   if (wave == 0) {
+    lds_wait(&L.misc[kVSortDone], kWaves, status);  // every zone sorted, every segment summed
     bool split_ready = nt == 0u;
     bool fail = false;
     uint32_t keep = keep_default;
