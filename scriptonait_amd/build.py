@@ -1,4 +1,5 @@
-"""Build step for the gfx950 sampler library (libllmhip_sampler.so).
+"""Build step for the gfx950 sampler library (libllmhip_sampler.so) and the
+read-floor probe (libllmhip_probe.so).
 
 Compiles the HIP sources under csrc/ with hipcc for gfx950 only, in-tree,
 so the built library travels with the source tree. Flags that matter for
@@ -26,6 +27,10 @@ CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libllmhip_sampler.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 SOURCES = ["sampler_kernels.hip", "sampler_api.hip"]
+# Measurement kernels (the streaming-read floor bench.py --read-floor reports);
+# not part of the sampler's ABI.
+PROBE_SOURCE = "read_probe.hip"
+PROBE_PATH = PKG_DIR / "libllmhip_probe.so"
 ARCH = "gfx950"
 
 
@@ -70,6 +75,12 @@ def build_library(verbose: bool = False) -> Path:
     os.replace(tmp, LIB_PATH)
     for o in objs:
         Path(o).unlink(missing_ok=True)
+    tmp = PROBE_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc, *compile_flags(), "-shared", "-o", str(tmp), str(CSRC / PROBE_SOURCE)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, PROBE_PATH)
     return LIB_PATH
 
 
