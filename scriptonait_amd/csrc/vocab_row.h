@@ -27,6 +27,11 @@
 // the bucket's elements that come before each tie, and the replay applies
 // round-half-even to the tie with the parity it then knows.
 //
+// The softmax sum runs alone (the other folds need S). The top-p cumulative
+// and the walk run together: one classification word per bucket for both,
+// one exact pass, one tie split and one zone sort, then the two replays one
+// after the other (the walk is classified for every start its total allows).
+//
 // Every assumption the approximate prefix made is checked exactly during the
 // replay; a row whose check fails, or that needs more zones than the LDS
 // holds, is handed to the sorting path (general_row), so the ids are the
@@ -45,7 +50,7 @@ namespace llmhip {
 constexpr uint32_t kVB = 4096;             // buckets
 constexpr float kVR = 128.0f;              // buckets per unit of y
 constexpr uint32_t kVZones = 320;          // zones (of either fold)
-constexpr uint32_t kVZoneEls = 4096;       // gathered elements per fold
+constexpr uint32_t kVZoneEls = 4096;       // gathered elements (of either fold)
 constexpr uint32_t kVTies = 256;           // ties in certain buckets (of either fold)
 constexpr uint32_t kVHash = 2048;          // repetition-count table slots
 constexpr uint32_t kVMaxDistinct = 1536;   // distinct history ids the table takes
