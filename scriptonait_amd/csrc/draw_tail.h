@@ -121,6 +121,149 @@ __device__ __forceinline__ void draw_tail(const SampleArgs& a, uint32_t b, uint3
   }
 }
 
+// The same computation for n <= 4096 candidates, with the terms staged in
+// LDS (`buf`: n rounded up to 64 floats, 16-byte aligned). Every fold is the
+// reference's left fold in f32, read as broadcast float4s: the softmax sum
+// 16 terms per step, top-p and the walk in blocks of 8 whose last value is
+// tested (c never decreases; r - p < 0 exactly when r < p), the block that
+// decides being resolved once, one lane per term. Terms past the kept
+// prefix are set to +0.0, which leaves either fold unchanged.
+// Must be called by all 64 lanes of exactly one wave.
+template <class KeyAt, class IdAt>
+__device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, uint32_t len_b, const llmhip_params& P,
+                                              uint32_t n, KeyAt key_at, IdAt id_at, uint64_t st, const uint64_t* tab,
+                                              float* buf) {
+  const uint32_t lane = lane_id();
+  const uint32_t k0 = key_at(0);
+  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);  // as in draw_tail
+  const uint32_t nr = (n + 63u) & ~63u;
+  for (uint32_t i = lane; i < nr; i += 64u) buf[i] = i < n ? glibc_expf_tab(key2f(key_at(i)) - mx, tab) : 0.0f;
+  const float4* b4 = reinterpret_cast<const float4*>(buf);
+  auto t8_at = [&](uint32_t base, float (&t8)[8]) __attribute__((always_inline)) {
+    const float4 lo = b4[base / 4u], hi = b4[base / 4u + 1u];
+    t8[0] = lo.x; t8[1] = lo.y; t8[2] = lo.z; t8[3] = lo.w;
+    t8[4] = hi.x; t8[5] = hi.y; t8[6] = hi.z; t8[7] = hi.w;
+  };
+
+  // generate.rs:374: sum = ((0 + e_0) + e_1) + ..., the next 16 terms
+  // loading while the current 16 are added.
+  float sum = 0.0f;
+  {
+    const uint32_t nq = nr / 4u;
+    float4 c0 = b4[0], c1 = b4[1], c2 = b4[2], c3 = b4[3];
+    for (uint32_t q = 0; q < nq; q += 4u) {
+      float4 d0 = c0, d1 = c1, d2 = c2, d3 = c3;
+      if (q + 4u < nq) {
+        d0 = b4[q + 4u];
+        d1 = b4[q + 5u];
+        d2 = b4[q + 6u];
+        d3 = b4[q + 7u];
+      }
+      sum += c0.x; sum += c0.y; sum += c0.z; sum += c0.w;
+      sum += c1.x; sum += c1.y; sum += c1.z; sum += c1.w;
+      sum += c2.x; sum += c2.y; sum += c2.z; sum += c2.w;
+      sum += c3.x; sum += c3.y; sum += c3.z; sum += c3.w;
+      c0 = d0; c1 = d1; c2 = d2; c3 = d3;
+    }
+  }
+  // generate.rs:375-377: degenerate exit, no draw.
+  if (!(sum > 0.0f) || !isfinite(sum)) {
+    if (lane == 0) {
+      store_result(a, b, id_at(0), len_b);
+      if (a.out_kept) a.out_kept[b] = 0u;
+    }
+    return;
+  }
+  for (uint32_t i = lane; i < n; i += 64u) buf[i] = buf[i] / sum;  // generate.rs:378-380
+
+  // generate.rs:384-395: longest prefix with p >= min_p * p_0, at least 1.
+  uint32_t keep = n;
+  if (P.min_p > 0.0f) {
+    const float thr = P.min_p * buf[0];
+    for (uint32_t c = 0; c < n; c += 64u) {
+      const uint32_t i = c + lane;
+      const uint64_t fail = __ballot(i < n && !(buf[i] >= thr));
+      if (fail) {
+        keep = c + (uint32_t)__ffsll((unsigned long long)fail) - 1u;
+        break;
+      }
+    }
+    if (keep < 1u) keep = 1u;
+  }
+  for (uint32_t i = keep + lane; i < nr; i += 64u) buf[i] = 0.0f;
+
+  // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; the cut is the first
+  // c_i >= top_p (all of the prefix when top_p >= 1 or never reached); the
+  // total is the fold at the last kept term.
+  uint32_t stop = keep;
+  float total;
+  {
+    const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
+    float c = 0.0f, cprev = 0.0f;
+    uint32_t k8 = 0u;
+    for (uint32_t base = 0; base < keep; base += 8u) {
+      float t8[8];
+      t8_at(base, t8);
+      cprev = c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c += t8[j];
+      k8 = base;
+      if (c >= tp) break;
+    }
+    // Lane j < 8 recomputes c_{k8+j} from the block's start, in order.
+    float t8[8], t = cprev;
+    t8_at(k8, t8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t = (uint32_t)j <= lane ? t + t8[j] : t;
+    const uint64_t hit = __ballot(lane < 8u && k8 + lane < keep && t >= tp);
+    if (hit) stop = k8 + (uint32_t)__ffsll((unsigned long long)hit);
+    total = readlane_f32(t, stop - 1u - k8);
+  }
+  // Terms past the cut leave the walk's r unchanged too.
+  for (uint32_t i = stop + lane; i < keep; i += 64u) buf[i] = 0.0f;
+
+  // generate.rs:412-419: r_0 = u * total; step i tests r_i < p_i, then
+  // subtracts p_i; no hit picks the last kept term.
+  const float u = next_f32(st);
+  uint32_t pick = stop - 1u;
+  {
+    float r = u * total, rprev = r;
+    uint32_t k8 = 0u;
+    bool neg = false;
+    for (uint32_t base = 0; base < stop; base += 8u) {
+      float t8[8];
+      t8_at(base, t8);
+      rprev = r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r -= t8[j];
+      k8 = base;
+      if (r < 0.0f) {
+        neg = true;
+        break;
+      }
+    }
+    if (neg) {
+      // Lane j < 8 recomputes r_{k8+j} (before its own subtraction).
+      float t8[8], t = rprev;
+      t8_at(k8, t8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t = (uint32_t)j < lane ? t - t8[j] : t;
+      const float pj = lane < 8u ? buf[k8 + lane] : 0.0f;
+      const uint64_t hit = __ballot(lane < 8u && k8 + lane < stop && t < pj);
+      if (hit) pick = k8 + (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+    }
+  }
+  if (lane == 0) {
+    store_result(a, b, id_at(pick), len_b);
+    a.rng_state[b] = st;
+    if (a.out_kept) a.out_kept[b] = stop;
+  }
+  if (a.out_probs) {
+    float* prow = a.out_probs + (size_t)b * a.V;
+    for (uint32_t i = lane; i < stop; i += 64u) prow[id_at(i)] = buf[i];
+  }
+}
+
 // Half an f32 ulp in the binade of x (x > 0; values below 2^-60 count as
 // 2^-60), as an f64.
 __device__ __forceinline__ double half_ulp_f32_at(double x) {

@@ -53,14 +53,20 @@
 
 namespace llmhip {
 
-// LDS needed by the general path (about 20 KB).
+// Top-k rows of the general path with K up to kSelCap are selected and
+// sorted in LDS; larger K sort the whole row in HBM scratch.
+constexpr uint32_t kSelCap = 4096;
+
+// LDS needed by the general path (about 53 KB).
 struct GenLds {
   uint32_t bins[256];
   uint32_t off[256];
-  uint32_t wc[kWaves * 256];
+  __attribute__((aligned(16))) uint32_t wc[kWaves * 256];  // also the tail's terms (<= kSelCap floats)
   float redv[kWaves];
   uint32_t redi[kWaves];
   uint64_t exptab[32];
+  uint64_t sel[kSelCap];  // the K selected order keys (key << 32 | ~id)
+  uint32_t sv[4];         // select state
 };
 
 constexpr uint32_t kFastCand = 2048;              // candidates per row
@@ -91,7 +97,7 @@ struct FastLds {
   __attribute__((aligned(16))) uint32_t fine[kFineBins];
   float4 ent[kWaves * kEntries];     // scan entries: a lane's 4 values of a chunk with a hit
   uint32_t etag[kWaves * kEntries];  // chunk position | hit mask << 24 | chunk << 28
-  uint64_t ord[kFastCand];   // settled order keys
+  __attribute__((aligned(16))) uint64_t ord[kFastCand];  // settled order keys; then the tail's terms
   uint32_t skey[kMaxFastK];  // sorted top-K: post-temperature key
   uint32_t sid[kMaxFastK];   //               id
   uint64_t exptab[32];
@@ -782,8 +788,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       draw_tail_bcast(a, b, len_b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u,
                       u_draw, st_next, L.exptab, L.tail);
     } else {
-      draw_tail(a, b, len_b, P, K, [&](uint32_t i) { return L.skey[i]; }, [&](uint32_t i) { return L.sid[i]; },
-                rng0, L.exptab);
+      draw_tail_lds(a, b, len_b, P, K, [&](uint32_t i) { return L.skey[i]; }, [&](uint32_t i) { return L.sid[i]; },
+                    rng0, L.exptab, reinterpret_cast<float*>(L.ord));
     }
   }
   LLMHIP_MARK(8);

@@ -23,6 +23,140 @@
 namespace llmhip {
 
 // ---------------------------------------------------------------------------
+// Top-k selection for the general path (0 < K <= kSelCap, K < V): the K
+// largest (key, id) pairs in the reference's order (key descending, ties by
+// ascending id, generate.rs:364-367), from the keys of a row in scratch.
+// ---------------------------------------------------------------------------
+
+// Order key: larger means earlier in the sorted order.
+__device__ __forceinline__ uint64_t sel_order(uint32_t key, uint32_t id) {
+  return ((uint64_t)key << 32) | (uint32_t)~id;
+}
+
+// The K-th largest key t, by an MSB-first radix select (digits of 11, 11
+// and 10 bits; bin counts from integer LDS atomics, so they do not depend on
+// the order of the adds), and r: how many of the K largest keys equal t
+// (1 <= r <= the count of t).
+__device__ __forceinline__ void select_kth(const uint32_t* keys, uint32_t V, uint32_t K, GenLds& L, uint32_t& t,
+                                           uint32_t& r) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  uint32_t* hist = L.wc;  // 2048 bins
+  uint32_t prefix = 0u, pmask = 0u, need = K;
+  for (uint32_t d = 0; d < 3u; ++d) {
+    const uint32_t bits = d < 2u ? 11u : 10u, shift = d == 0u ? 21u : d == 1u ? 10u : 0u;
+    const uint32_t nb = 1u << bits, per = nb / 64u;
+    for (uint32_t i = tid; i < nb; i += kBlock) hist[i] = 0u;
+    __syncthreads();
+    for (uint32_t i0 = tid; i0 < V; i0 += 8u * kBlock) {
+      uint32_t k[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) k[u] = i0 + u * kBlock < V ? keys[i0 + u * kBlock] : 0u;
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u)
+        if (i0 + u * kBlock < V && (k[u] & pmask) == prefix) atomicAdd(&hist[(k[u] >> shift) & (nb - 1u)], 1u);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // Lane l holds bins top .. top - per + 1 (descending); the class holds
+      // at least `need` keys, so some lane's inclusive count reaches it.
+      const uint32_t top = nb - 1u - per * lane;
+      uint32_t s = 0u;
+      for (uint32_t j = 0; j < per; ++j) s += hist[top - j];
+      const uint32_t inc = wave_incl_scan(s);
+      const uint32_t l = (uint32_t)__ffsll((unsigned long long)__ballot(inc >= need)) - 1u;
+      if (lane == l) {
+        uint32_t c = inc - s, dg = top;
+        for (uint32_t j = 0; j < per; ++j) {
+          const uint32_t h = hist[top - j];
+          if (c + h >= need) {
+            dg = top - j;
+            break;
+          }
+          c += h;
+        }
+        L.sv[0] = dg;
+        L.sv[1] = c;
+      }
+    }
+    __syncthreads();
+    need -= L.sv[1];
+    prefix |= L.sv[0] << shift;
+    pmask |= (nb - 1u) << shift;
+    __syncthreads();  // sv and the bins are rewritten by the next digit
+  }
+  t = prefix;
+  r = need;
+}
+
+// L.sel[0, K) = the K largest order keys, sorted descending.
+__device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uint32_t K, GenLds& L) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  uint32_t t, r;
+  select_kth(keys, V, K, L, t, r);
+  // Every key above t goes to [0, K - r) in any order (the sort below
+  // orders them); thread tid walks ids [tid*S, tid*S + S) and counts its
+  // keys equal to t.
+  if (tid == 0) L.sv[2] = 0u;
+  __syncthreads();
+  const uint32_t S = (V + kBlock - 1u) / kBlock;
+  const uint32_t i0 = tid * S, i1 = min(V, i0 + S);
+  uint32_t ties = 0u;
+  for (uint32_t j0 = 0; j0 < S; j0 += 8u) {
+    uint32_t kb[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) kb[u] = i0 + j0 + u < i1 ? keys[i0 + j0 + u] : 0u;
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t i = i0 + j0 + u, k = kb[u];
+      const bool above = i < i1 && k > t;
+      ties += (i < i1 && k == t) ? 1u : 0u;
+      const uint64_t m = __ballot(above);
+      if (m) {
+        uint32_t o = 0u;
+        if (lane == 0) o = atomicAdd(&L.sv[2], (uint32_t)__popcll((unsigned long long)m));
+        o = readlane_u32(o, 0) + lanes_below(m);
+        if (above) L.sel[o] = sel_order(k, i);
+      }
+    }
+  }
+  // The r lowest ids among the keys equal to t: a block scan of the
+  // per-thread counts (threads hold ascending id ranges) places them at
+  // [K - r, K).
+  const uint32_t winc = wave_incl_scan(ties);
+  if (lane == 63u) L.bins[wave] = winc;
+  __syncthreads();
+  uint32_t rank = winc - ties;
+  for (uint32_t w = 0; w < wave; ++w) rank += L.bins[w];
+  if (ties != 0u && rank < r) {
+    for (uint32_t i = i0; i < i1 && rank < r; ++i) {
+      if (keys[i] == t) {
+        L.sel[K - r + rank] = sel_order(t, i);
+        ++rank;
+      }
+    }
+  }
+  // Bitonic sort, descending, over N = the power of two >= K (padding 0 sorts
+  // last: every real order key is above 0). The order keys are distinct.
+  uint32_t N = 1u;
+  while (N < K) N <<= 1;
+  for (uint32_t i = K + tid; i < N; i += kBlock) L.sel[i] = 0ull;
+  __syncthreads();
+  for (uint32_t k = 2u; k <= N; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
+      for (uint32_t p = tid; p < N / 2u; p += kBlock) {
+        const uint32_t i = ((p & ~(j - 1u)) << 1) | (p & (j - 1u));
+        const uint64_t x = L.sel[i], y = L.sel[i | j];
+        if ((i & k) == 0u ? x < y : x > y) {
+          L.sel[i] = y;
+          L.sel[i | j] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // General path: one row, 1024 threads, scratch in HBM.
 // Scratch per row (Vp = V rounded up to 1024): keysA | idsA | keysB | idsB | cnt
 // ---------------------------------------------------------------------------
@@ -71,20 +205,38 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
 
   const bool greedy = P.temperature <= 0.0f;
   const float T = P.temperature, rp = P.repetition_penalty;
+  const uint32_t n = (P.top_k > 0 && P.top_k < V) ? P.top_k : V;
+  const bool sel = n < V && n <= kSelCap;  // a top-k row whose K fits the LDS list
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
-  for (uint32_t i = tid; i < V; i += kBlock) {
-    float v = row[i];
-    if (masked_out(a, i)) v = -INFINITY;
-    if (use_pen) v = apply_penalty(v, __hip_atomic_load(&cnt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), rp);
-    if (greedy) {
-      if (v > bv) {
-        bv = v;
-        bi = i;
+  // Eight elements per thread in flight: their loads go out before any use.
+  for (uint32_t i0 = tid; i0 < V; i0 += 8u * kBlock) {
+    float xv[8];
+    uint32_t mc[8];
+    bool mo[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t i = i0 + u * kBlock;
+      xv[u] = i < V ? row[i] : 0.0f;
+      mc[u] = (use_pen && i < V) ? __hip_atomic_load(&cnt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      mo[u] = i < V && masked_out(a, i);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t i = i0 + u * kBlock;
+      if (i >= V) break;
+      float v = xv[u];
+      if (mo[u]) v = -INFINITY;
+      if (use_pen) v = apply_penalty(v, mc[u], rp);
+      if (greedy) {
+        if (v > bv) {
+          bv = v;
+          bi = i;
+        }
+      } else {
+        keysA[i] = f2key(v / T);
+        if (!sel) idsA[i] = i;
       }
-    } else {
-      keysA[i] = f2key(v / T);
-      idsA[i] = i;
     }
   }
   if (greedy) {
@@ -96,6 +248,15 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
     return;
   }
   __syncthreads();
+  if (sel) {
+    select_top(keysA, V, n, L);
+    if (wave == 0) {
+      draw_tail_lds(a, b, len_b, P, n, [&](uint32_t i) { return (uint32_t)(L.sel[i] >> 32); },
+                    [&](uint32_t i) { return ~(uint32_t)L.sel[i]; }, a.rng_state[b], L.exptab,
+                    reinterpret_cast<float*>(L.wc));
+    }
+    return;
+  }
 
   // Stable LSD radix sort, 4 x 8-bit digits, descending: ties keep
   // ascending id, which is the reference's order (generate.rs:364-367).
@@ -156,10 +317,13 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
     }
   }
   // Four passes end in A.
-  const uint32_t n = (P.top_k > 0 && P.top_k < V) ? P.top_k : V;
   if (wave == 0) {
-    draw_tail(a, b, len_b, P, n, [&](uint32_t i) { return keysA[i]; }, [&](uint32_t i) { return idsA[i]; },
-              a.rng_state[b], L.exptab);
+    auto key_at = [&](uint32_t i) { return keysA[i]; };
+    auto id_at = [&](uint32_t i) { return idsA[i]; };
+    if (n <= kSelCap)
+      draw_tail_lds(a, b, len_b, P, n, key_at, id_at, a.rng_state[b], L.exptab, reinterpret_cast<float*>(L.wc));
+    else
+      draw_tail(a, b, len_b, P, n, key_at, id_at, a.rng_state[b], L.exptab);
   }
 }
 

@@ -1,0 +1,100 @@
+"""GPU: top-k rows of the sorting path against the oracle.
+
+Rows with 1024 < top_k <= 4096 (and rows the fast kernel hands over) select
+the K largest keys by a radix select and sort them in LDS; larger K sort the
+whole row in HBM scratch. Both must give the reference's order: key
+descending, ties by ascending id (crates/llm-core/src/generate.rs:364-367).
+"""
+import numpy as np
+import pytest
+
+from parity_util import compare, run_both
+from scriptonait_amd.workloads import make_params, make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("k", [1025, 2000, 4096, 4097, 20000, 31999])
+def test_top_k_above_the_fast_limit(sampler, k):
+    w = make_workload(3, B=16)
+    prm = make_params(0.7, k, 0.95, 0.0, 1.15)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, f"k={k}")
+
+
+@pytest.mark.parametrize("k", [1100, 3000])
+def test_top_k_select_with_ties_at_the_cut(sampler, k):
+    """Logits on a coarse grid: the K-th key is shared by hundreds of ids, of
+    which only the lowest ids are kept."""
+    w = make_workload(3, B=16)
+    w.logits[:] = np.round(w.logits * 2.0) / 2.0
+    prm = make_params(1.3, k, 1.0, 0.0, 1.0)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, f"quantized k={k}")
+
+
+def test_top_k_select_fewer_allowed_than_k(sampler):
+    """Only 700 ids allowed and K = 2000: the cut falls among the -inf keys."""
+    w = make_workload(3, B=8)
+    allowed = np.zeros(w.V, dtype=np.uint8)
+    allowed[np.random.default_rng(3).choice(w.V, 700, replace=False)] = 1
+    prm = make_params(0.9, 2000, 0.9, 0.02, 1.2)
+    g, o = run_both(sampler, w, params=prm, allowed=allowed)
+    compare(g, o, "700 allowed, k=2000")
+
+
+@pytest.mark.parametrize("k", [1, 64, 1000])
+def test_hand_over_rows_penalty_below_one(sampler, k):
+    """A penalty below 1 can raise a value, so the fast kernel hands these
+    rows to the sorting path (which selects in LDS)."""
+    w = make_workload(3, B=16)
+    prm = make_params(0.8, k, 0.95, 0.05, 0.85)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, f"rp<1 k={k}")
+
+
+@pytest.mark.parametrize("V,k", [(4097, 4096), (5000, 4999), (40000, 3000), (131072, 4000)])
+def test_top_k_select_other_vocab_sizes(sampler, V, k):
+    w = make_workload(3, B=4, V=V)
+    prm = make_params(1.0, k, 0.98, 0.01, 1.1)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, f"V={V} k={k}")
+
+
+@pytest.mark.parametrize("k", [65, 128, 700, 1024])
+@pytest.mark.parametrize("filters", [(0.7, 0.95, 0.05, 1.15), (1.0, 1.0, 0.0, 1.0)])
+def test_fast_kernel_k_above_64(sampler, k, filters):
+    """64 < K <= 1024 stays in the fast kernel; its tail folds the terms from LDS."""
+    T, top_p, min_p, rp = filters
+    w = make_workload(3, B=32)
+    prm = make_params(T, k, top_p, min_p, rp)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, f"k={k} filters={filters}")
+
+
+@pytest.mark.parametrize("K", [128, 2000])
+def test_exact_ties_in_the_lds_tail_folds(sampler, K):
+    """128 equal top values give p_i = 1/128 and exact cumulative sums: top-p
+    cuts and draws that land exactly on a fold value, decided by the exact
+    f32 folds of the LDS tail (generate.rs:397-419)."""
+    from oracle import oracle
+    from scriptonait_amd.workloads import PARAMS_DTYPE
+    from test_gpu_parity import _seed_for_draw
+
+    rs = np.random.default_rng(11)
+    B, V = 64, 32000
+    logits = (rs.standard_normal((B, V)) - 20.0).astype(np.float32)
+    for b in range(B):
+        logits[b, rs.choice(V, 128, replace=False)] = 5.0
+    prm = np.zeros(B, dtype=PARAMS_DTYPE)
+    seeds = np.zeros(B, dtype=np.uint64)
+    for b in range(B):
+        top_p = [0.5, 0.25, 1.0, 0.75 + 2.0 ** -20][b % 4]
+        prm[b] = (1.0, K, top_p, [0.0, 0.5][b % 2], 1.0)
+        seeds[b] = _seed_for_draw((b % 32) << 19)  # u = (b % 32) / 32
+    g = sampler.sample_host(logits, prm, seeds, want_probs=True)
+    o = oracle.sample_batch(logits, prm, seeds, want_probs=True)
+    assert np.array_equal(g.ids, o.ids), np.nonzero(g.ids != o.ids)[0]
+    assert np.array_equal(g.kept, o.kept)
+    assert np.array_equal(g.rng_state, o.rng_state)
+    assert np.array_equal(g.probs, o.probs)
