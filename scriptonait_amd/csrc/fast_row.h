@@ -367,21 +367,38 @@ __device__ __forceinline__ void rank_in_regs(const uint64_t* ord, uint32_t n, ui
   }
 }
 
-__device__ __forceinline__ void rank_in_lds(const uint64_t* ord, uint32_t n, uint32_t K, uint32_t wave,
-                                            uint32_t lane, uint32_t* skey, uint32_t* sid) {
-  const uint32_t per = (n + kWaves - 1) / kWaves;
-  const uint32_t i0 = min(n, wave * per), i1 = min(n, i0 + per);
-  for (uint32_t i = i0; i < i1; ++i) {
-    const uint64_t oi = ord[i];
-    uint32_t r = 0u;
-    for (uint32_t j0 = 0; j0 < n; j0 += 64) {
-      const uint32_t j = j0 + lane;
-      r += (uint32_t)__popcll((unsigned long long)__ballot(j < n && ord[j] > oi));
+// Sorts v[0, n) descending in place (all threads of the workgroup): a
+// bitonic network over N = the power of two >= n, with v[n, N) set to 0,
+// which sorts last (every order key here is above 0). v holds at least N
+// entries. The order keys are distinct, so the order is the total one.
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t* v, uint32_t n) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t N = 1u;
+  while (N < n) N <<= 1;
+  for (uint32_t i = n + tid; i < N; i += kBlock) v[i] = 0ull;
+  lds_barrier();
+  for (uint32_t k = 2u; k <= N; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
+      for (uint32_t p = tid; p < N / 2u; p += kBlock) {
+        const uint32_t i = ((p & ~(j - 1u)) << 1) | (p & (j - 1u));  // bit j of i clear
+        const uint64_t x = v[i], y = v[i | j];
+        if ((i & k) == 0u ? x < y : x > y) {
+          v[i] = y;
+          v[i | j] = x;
+        }
+      }
+      lds_barrier();
     }
-    if (r < K && lane == 0) {
-      skey[r] = (uint32_t)(oi >> 32);
-      sid[r] = 0xffffffffu - (uint32_t)oi;
-    }
+  }
+}
+
+// More candidates than the register ranks hold (n <= kFastCand): sort them.
+__device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint32_t n, uint32_t K, uint32_t* skey, uint32_t* sid) {
+  bitonic_sort_desc(ord, n);
+  for (uint32_t i = threadIdx.x; i < K; i += kBlock) {
+    const uint64_t o = ord[i];
+    skey[i] = (uint32_t)(o >> 32);
+    sid[i] = 0xffffffffu - (uint32_t)o;
   }
 }
 
@@ -776,7 +793,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   } else if (n <= 512) {
     rank_in_regs<8>(L.ord, n, K, wave, lane, L.skey, L.sid);
   } else {
-    rank_in_lds(L.ord, n, K, wave, lane, L.skey, L.sid);
+    rank_in_lds(L.ord, n, K, L.skey, L.sid);
   }
   LLMHIP_MARK(10);
   lds_barrier();

@@ -135,25 +135,7 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
       }
     }
   }
-  // Bitonic sort, descending, over N = the power of two >= K (padding 0 sorts
-  // last: every real order key is above 0). The order keys are distinct.
-  uint32_t N = 1u;
-  while (N < K) N <<= 1;
-  for (uint32_t i = K + tid; i < N; i += kBlock) L.sel[i] = 0ull;
-  __syncthreads();
-  for (uint32_t k = 2u; k <= N; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
-      for (uint32_t p = tid; p < N / 2u; p += kBlock) {
-        const uint32_t i = ((p & ~(j - 1u)) << 1) | (p & (j - 1u));
-        const uint64_t x = L.sel[i], y = L.sel[i | j];
-        if ((i & k) == 0u ? x < y : x > y) {
-          L.sel[i] = y;
-          L.sel[i | j] = x;
-        }
-      }
-      __syncthreads();
-    }
-  }
+  bitonic_sort_desc(L.sel, K);  // its first barrier completes the list
 }
 
 // ---------------------------------------------------------------------------
