@@ -42,6 +42,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", type=int, default=3, help="workload config 1..5 (3 = headline)")
     ap.add_argument("--batch", type=int, default=None, help="override B (not for the headline line)")
+    ap.add_argument("--top-k", type=int, default=None,
+                    help="override every row's top_k (not for the headline line)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -171,6 +173,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     w = make_workload(args.config, B=args.batch)
+    if args.top_k is not None:
+        params = w.params.copy()
+        params["top_k"] = args.top_k
+        w.params = params
     sampler = Sampler(0)
 
     # Device-resident input sets, rotated so each launch misses the MALL.
@@ -227,7 +233,7 @@ def main():
 
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{w.name}.json"
-    if tf.exists():
+    if tf.exists() and args.top_k is None and args.batch is None:
         try:
             traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
         except Exception:
@@ -259,6 +265,7 @@ def main():
             "B": w.B,
             "V": w.V,
             "bytes_per_row": w.bytes_per_row(),
+            **({"top_k": args.top_k} if args.top_k is not None else {}),
         },
         "achieved_gbs": achieved,
         "pct_of_peak_hbm": 100.0 * achieved / PEAK_HBM_GBS,
