@@ -264,6 +264,163 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
   }
 }
 
+// The same computation for any n, with the terms staged in LDS windows of
+// `cap` floats (a multiple of 64; `buf` 16-byte aligned): each fold runs
+// over the windows in order with its value carried from one to the next,
+// and a window's terms are recomputed from the keys when it is staged.
+// Used where n exceeds what one window holds.
+template <class KeyAt, class IdAt>
+__device__ __forceinline__ void draw_tail_win(const SampleArgs& a, uint32_t b, uint32_t len_b, const llmhip_params& P,
+                                              uint32_t n, KeyAt key_at, IdAt id_at, uint64_t st, const uint64_t* tab,
+                                              float* buf, uint32_t cap) {
+  const uint32_t lane = lane_id();
+  const uint32_t k0 = key_at(0);
+  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);  // as in draw_tail
+  auto e_at = [&](uint32_t i) { return glibc_expf_tab(key2f(key_at(i)) - mx, tab); };
+  const float4* b4 = reinterpret_cast<const float4*>(buf);
+  // buf[j] = the term of i = w0 + j for i < lim (e_i, or e_i / div when div
+  // is not 0), +0.0 up to the next multiple of 64. Returns the count staged.
+  auto stage = [&](uint32_t w0, uint32_t lim, float div) __attribute__((always_inline)) {
+    const uint32_t cnt = min(cap, lim - w0), cr = (cnt + 63u) & ~63u;
+    for (uint32_t j = lane; j < cr; j += 64u) {
+      float t = 0.0f;
+      if (j < cnt) {
+        t = e_at(w0 + j);
+        if (div != 0.0f) t = t / div;
+      }
+      buf[j] = t;
+    }
+    return cnt;
+  };
+  auto t8_at = [&](uint32_t base, float (&t8)[8]) __attribute__((always_inline)) {
+    const float4 lo = b4[base / 4u], hi = b4[base / 4u + 1u];
+    t8[0] = lo.x; t8[1] = lo.y; t8[2] = lo.z; t8[3] = lo.w;
+    t8[4] = hi.x; t8[5] = hi.y; t8[6] = hi.z; t8[7] = hi.w;
+  };
+
+  // generate.rs:374: the softmax sum as one left fold over the windows.
+  float sum = 0.0f;
+  for (uint32_t w0 = 0; w0 < n; w0 += cap) {
+    const uint32_t cnt = stage(w0, n, 0.0f);
+    for (uint32_t base = 0; base < cnt; base += 8u) {
+      float t8[8];
+      t8_at(base, t8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum += t8[j];
+    }
+  }
+  // generate.rs:375-377: degenerate exit, no draw.
+  if (!(sum > 0.0f) || !isfinite(sum)) {
+    if (lane == 0) {
+      store_result(a, b, id_at(0), len_b);
+      if (a.out_kept) a.out_kept[b] = 0u;
+    }
+    return;
+  }
+  auto p_at = [&](uint32_t i) { return e_at(i) / sum; };  // generate.rs:378-380
+
+  // generate.rs:384-395: longest prefix with p >= min_p * p_0, at least 1.
+  uint32_t keep = n;
+  if (P.min_p > 0.0f) {
+    const float thr = P.min_p * p_at(0);
+    for (uint32_t c = 0; c < n; c += 64u) {
+      const uint32_t i = c + lane;
+      const uint64_t fail = __ballot(i < n && !(p_at(i) >= thr));
+      if (fail) {
+        keep = c + (uint32_t)__ffsll((unsigned long long)fail) - 1u;
+        break;
+      }
+    }
+    if (keep < 1u) keep = 1u;
+  }
+
+  // generate.rs:397-411: the top-p fold over the kept prefix, in blocks of 8
+  // (c never decreases); the deciding block is resolved one lane per term.
+  uint32_t stop = keep;
+  float total = 0.0f;
+  {
+    const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
+    float c = 0.0f;
+    bool hit_any = false;
+    for (uint32_t w0 = 0; w0 < keep && !hit_any; w0 += cap) {
+      const uint32_t cnt = stage(w0, keep, sum);
+      float cprev = 0.0f;
+      uint32_t k8 = 0u;
+      bool brk = false;
+      for (uint32_t base = 0; base < cnt; base += 8u) {
+        float t8[8];
+        t8_at(base, t8);
+        cprev = c;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c += t8[j];
+        k8 = base;
+        if (c >= tp) {
+          brk = true;
+          break;
+        }
+      }
+      if (brk) {
+        float t8[8], t = cprev;
+        t8_at(k8, t8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t = (uint32_t)j <= lane ? t + t8[j] : t;
+        const uint64_t hit = __ballot(lane < 8u && k8 + lane < cnt && t >= tp);
+        const uint32_t h = (uint32_t)__ffsll((unsigned long long)hit);  // a hit exists: c >= tp
+        stop = w0 + k8 + h;
+        total = readlane_f32(t, h - 1u);
+        hit_any = true;
+      }
+    }
+    if (!hit_any) total = c;  // the padding adds +0.0
+  }
+
+  // generate.rs:412-419: r_0 = u * total; step i tests r_i < p_i, then
+  // subtracts p_i; no hit picks the last kept term.
+  const float u = next_f32(st);
+  uint32_t pick = stop - 1u;
+  {
+    float r = u * total;
+    bool found = false;
+    for (uint32_t w0 = 0; w0 < stop && !found; w0 += cap) {
+      const uint32_t cnt = stage(w0, stop, sum);
+      float rprev = r;
+      uint32_t k8 = 0u;
+      bool neg = false;
+      for (uint32_t base = 0; base < cnt; base += 8u) {
+        float t8[8];
+        t8_at(base, t8);
+        rprev = r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r -= t8[j];
+        k8 = base;
+        if (r < 0.0f) {
+          neg = true;
+          break;
+        }
+      }
+      if (neg) {
+        float t8[8], t = rprev;
+        t8_at(k8, t8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t = (uint32_t)j < lane ? t - t8[j] : t;
+        const float pj = lane < 8u ? buf[k8 + lane] : 0.0f;
+        const uint64_t hit = __ballot(lane < 8u && k8 + lane < cnt && t < pj);
+        if (hit) pick = w0 + k8 + (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+        found = true;
+      }
+    }
+  }
+  if (lane == 0) {
+    store_result(a, b, id_at(pick), len_b);
+    a.rng_state[b] = st;
+    if (a.out_kept) a.out_kept[b] = stop;
+  }
+  if (a.out_probs) {
+    float* prow = a.out_probs + (size_t)b * a.V;
+    for (uint32_t i = lane; i < stop; i += 64u) prow[id_at(i)] = p_at(i);
+  }
+}
+
 // Half an f32 ulp in the binade of x (x > 0; values below 2^-60 count as
 // 2^-60), as an f64.
 __device__ __forceinline__ double half_ulp_f32_at(double x) {

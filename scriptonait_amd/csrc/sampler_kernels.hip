@@ -242,6 +242,13 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
 
   // Stable LSD radix sort, 4 x 8-bit digits, descending: ties keep
   // ascending id, which is the reference's order (generate.rs:364-367).
+  // Blocks of 1024 elements are ranked in order: per wave, the lanes with
+  // the same digit are found by 8 ballots; 256 threads then turn the
+  // per-wave digit counts into scatter offsets (wo), so an element's
+  // position is one LDS read. Eight blocks' keys and ids are loaded at a
+  // time; inside a pass the barriers order LDS only (the scatter's global
+  // stores are waited for at the next pass's full barrier).
+  uint32_t* wo = reinterpret_cast<uint32_t*>(L.sel);  // kWaves * 256 offsets
   for (uint32_t pass = 0; pass < 4; ++pass) {
     const uint32_t shift = 8u * pass;
     const uint32_t* sK = (pass & 1) ? keysB : keysA;
@@ -251,7 +258,14 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
     if (tid < 256) L.bins[tid] = 0u;
     for (uint32_t i = tid; i < kWaves * 256; i += kBlock) L.wc[i] = 0u;
     __syncthreads();
-    for (uint32_t i = tid; i < V; i += kBlock) atomicAdd(&L.bins[(sK[i] >> shift) & 255u], 1u);
+    for (uint32_t i0 = tid; i0 < V; i0 += 8u * kBlock) {
+      uint32_t k[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) k[u] = i0 + u * kBlock < V ? sK[i0 + u * kBlock] : 0u;
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u)
+        if (i0 + u * kBlock < V) atomicAdd(&L.bins[(k[u] >> shift) & 255u], 1u);
+    }
     __syncthreads();
     if (wave == 0) {
       const uint32_t d0 = 255u - 4u * lane;
@@ -264,39 +278,50 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
       L.off[d0 - 3] = ex + c0 + c1 + c2;
     }
     __syncthreads();
-    for (uint32_t base = 0; base < V; base += kBlock) {
-      const uint32_t i = base + tid;
-      const bool valid = i < V;
-      const uint32_t k = valid ? sK[i] : 0u;
-      const uint32_t id = valid ? sI[i] : 0u;
-      const uint32_t d = (k >> shift) & 255u;
-      uint64_t m = __ballot(valid);
+    for (uint32_t g0 = 0; g0 < V; g0 += 8u * kBlock) {
+      uint32_t kg[8], ig[8];
 #pragma unroll
-      for (uint32_t bit = 0; bit < 8; ++bit) {
-        const bool s = (d >> bit) & 1u;
-        const uint64_t bb = __ballot(s);
-        m &= s ? bb : ~bb;
+      for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t i = g0 + u * kBlock + tid;
+        kg[u] = i < V ? sK[i] : 0u;
+        ig[u] = i < V ? sI[i] : 0u;
       }
-      const uint32_t rank = (uint32_t)__popcll(m & lanemask_lt());
-      if (valid && rank == 0) L.wc[wave * 256 + d] = (uint32_t)__popcll(m);
-      __syncthreads();
-      if (valid) {
-        uint32_t pos = L.off[d] + rank;
-        for (uint32_t w = 0; w < wave; ++w) pos += L.wc[w * 256 + d];
-        dK[pos] = k;
-        dI[pos] = id;
-      }
-      __syncthreads();
-      if (tid < 256) {
-        uint32_t s = 0;
-        for (uint32_t w = 0; w < kWaves; ++w) {
-          s += L.wc[w * 256 + tid];
-          L.wc[w * 256 + tid] = 0u;
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t base = g0 + u * kBlock;
+        if (base >= V) break;
+        const bool valid = base + tid < V;
+        const uint32_t k = kg[u], id = ig[u];
+        const uint32_t d = (k >> shift) & 255u;
+        uint64_t m = __ballot(valid);
+#pragma unroll
+        for (uint32_t bit = 0; bit < 8; ++bit) {
+          const bool s = (d >> bit) & 1u;
+          const uint64_t bb = __ballot(s);
+          m &= s ? bb : ~bb;
         }
-        L.off[tid] += s;
+        const uint32_t rank = (uint32_t)__popcll(m & lanemask_lt());
+        if (valid && rank == 0) L.wc[wave * 256 + d] = (uint32_t)__popcll(m);
+        lds_barrier();
+        if (tid < 256) {
+          uint32_t run = L.off[tid];
+          for (uint32_t w = 0; w < kWaves; ++w) {
+            const uint32_t c = L.wc[w * 256 + tid];
+            wo[w * 256 + tid] = run;
+            L.wc[w * 256 + tid] = 0u;
+            run += c;
+          }
+          L.off[tid] = run;
+        }
+        lds_barrier();
+        if (valid) {
+          const uint32_t pos = wo[wave * 256 + d] + rank;
+          dK[pos] = k;
+          dI[pos] = id;
+        }
       }
-      __syncthreads();
     }
+    __syncthreads();  // the scatter's stores, before the next pass reads them
   }
   // Four passes end in A.
   if (wave == 0) {
@@ -305,7 +330,8 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
     if (n <= kSelCap)
       draw_tail_lds(a, b, len_b, P, n, key_at, id_at, a.rng_state[b], L.exptab, reinterpret_cast<float*>(L.wc));
     else
-      draw_tail(a, b, len_b, P, n, key_at, id_at, a.rng_state[b], L.exptab);
+      draw_tail_win(a, b, len_b, P, n, key_at, id_at, a.rng_state[b], L.exptab, reinterpret_cast<float*>(L.wc),
+                    kSelCap);
   }
 }
 

@@ -72,11 +72,12 @@ def test_fast_kernel_k_above_64(sampler, k, filters):
     compare(g, o, f"k={k} filters={filters}")
 
 
-@pytest.mark.parametrize("K", [128, 2000])
+@pytest.mark.parametrize("K", [128, 2000, 6000])
 def test_exact_ties_in_the_lds_tail_folds(sampler, K):
     """128 equal top values give p_i = 1/128 and exact cumulative sums: top-p
     cuts and draws that land exactly on a fold value, decided by the exact
-    f32 folds of the LDS tail (generate.rs:397-419)."""
+    f32 folds of the LDS tail (generate.rs:397-419); K = 6000 folds over two
+    LDS windows."""
     from oracle import oracle
     from scriptonait_amd.workloads import PARAMS_DTYPE
     from test_gpu_parity import _seed_for_draw
