@@ -687,12 +687,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   LLMHIP_MARK(5);
 
   // 5. Settle this wave's entries: each lane takes an entry and handles its
-  //    hits one at a time (almost always one): mask, penalty, recheck
-  //    (final == false), then the post-temperature order key (one
+  //    hits one at a time (almost always one): mask, penalty, recheck,
+  //    then the post-temperature order key (one
   //    division, generate.rs:357-359), appended to ord[] with one LDS
   //    atomic per round.
   uint32_t pmv = 0u;
-  auto settle = [&](bool final) __attribute__((always_inline)) {
+  auto settle = [&]() __attribute__((always_inline)) {
     if (__builtin_expect(nent > kEntries, 0)) {
       if (lane == 0) atomicOr(&L.misc[kOverflow], 1u);
       return;
@@ -711,8 +711,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
                               : 0u;
       // The entry's owner is a lane of this wave: fetch its mask words.
       const uint32_t owner = pos_owner<NCH>(base);
-      const uint32_t mkown = final ? 0u : (uint32_t)__builtin_amdgcn_ds_bpermute((int)((owner & 63u) << 2), (int)mkbits);
-      const uint32_t pmown = (final || !use_pen || k >= nent) ? 0u : L.pm[owner];
+      const uint32_t mkown = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((owner & 63u) << 2), (int)mkbits);
+      const uint32_t pmown = (!use_pen || k >= nent) ? 0u : L.pm[owner];
       while (__ballot(rem != 0u)) {
         // A lane takes part in a round only while it has a hit left.
         bool ok = rem != 0u;
@@ -720,7 +720,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
         rem &= rem - 1u;
         float v = j == 0 ? ev.x : j == 1 ? ev.y : j == 2 ? ev.z : ev.w;
         const uint32_t e = 4u * c + j, pos = base + j;
-        if (ok && !final) {
+        if (ok) {
           if ((mkown >> e) & 1u) v = -INFINITY;
           if ((pmown >> e) & 1u) v = apply_penalty(v, count_of(pos), rp);
           ok = v >= tf;
@@ -739,7 +739,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     lds_wait(&L.misc[kSyncHist], kTauWaves, a.status);
     pmv = L.pm[tid];
   }
-  settle(false);
+  settle();
   lds_barrier();
   LLMHIP_MARK(6);
   uint32_t n = L.misc[kCandN];
@@ -771,15 +771,25 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, K, true, lane), T, lane);
     if (tkey == 0u) return false;
     tf = key2f(tkey);
-    // Values are final now (fixed in place).
-    nent = 0u;
+    // Values are final now (fixed in place): every lane appends its own
+    // values at or above the threshold, one ballot per slot, with no scan
+    // entries (so no per-wave region can overflow).
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) scan_chunk(c, max4(c));
-    settle(true);
+    for (int e = 0; e < NCH * 4; ++e) {
+      const bool ok = x[e] >= tf;
+      const uint64_t mk = __ballot(ok);
+      if (mk) {
+        uint32_t o = 0u;
+        if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
+        o = readlane_u32(o, 0) + lanes_below(mk);
+        if (ok && o < kFastCand)
+          L.ord[o] = cand_order(f2key(x[e] / T), chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3));
+      }
+    }
     lds_barrier();
     n = L.misc[kCandN];
     // Heavy ties or an unusually flat top: not bounded by the register path.
-    if (n < K || n > kFastCand || L.misc[kOverflow]) return false;
+    if (n < K || n > kFastCand) return false;
   }
 
   // 6. Ranks by (w key desc, id asc).
