@@ -47,9 +47,6 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
-    ap.add_argument("--read-floor", action="store_true",
-                    help="instead of benchmarking, measure the achievable streaming-read floor for the "
-                         "workload's shape (a read-only kernel with the fast kernel's loads)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of benchmarking, run 10 device-to-device copies of MIB MiB "
                          "(a plain copy kernel of known size, to scale rocprofv3 byte counters)")
@@ -68,54 +65,6 @@ def calibrate_copy(mib: int) -> None:
     torch.cuda.synchronize()
     print(json.dumps({"calibrate_copy_bytes_read": n, "calibrate_copy_bytes_written": n,
                       "copies": 10}), flush=True)
-
-
-def read_floor(args) -> None:
-    """Time the read-only probe kernel (the fast kernel's access shape, one
-    1024-thread workgroup per row, nontemporal dwordx4 loads) over the same
-    rotating input sets as the bench, back to back like the bench's steps."""
-    import ctypes
-
-    import torch
-
-    from scriptonait_amd.build import PROBE_PATH
-    from scriptonait_amd.workloads import make_workload
-
-    lib = ctypes.CDLL(str(PROBE_PATH))
-    vp, sz = ctypes.c_void_p, ctypes.c_size_t
-    lib.llmhip_probe_read.argtypes = [vp, sz, sz, sz, vp, vp]
-    w = make_workload(args.config, B=args.batch)
-    dev = torch.device("cuda:0")
-    base = torch.from_numpy(w.logits).to(dev)
-    n_sets = max(2, int(np.ceil(2 * MALL_BYTES / (w.B * w.ld * 4))) + 1)
-    sets = [torch.roll(base, k, 0).contiguous() for k in range(n_sets)]
-    out = torch.zeros(w.B, dtype=torch.float32, device=dev)
-    st = torch.cuda.current_stream()
-
-    def timed(fn) -> float:
-        for i in range(args.warmup):
-            fn(i)
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(st)
-        for i in range(args.steps):
-            fn(i)
-        b.record(st)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) * 1e3 / args.steps
-
-    def rd(i):
-        rc = lib.llmhip_probe_read(sets[i % n_sets].data_ptr(), w.B, w.V, w.ld, out.data_ptr(), st.cuda_stream)
-        assert rc == 0, rc
-
-    us_read = timed(rd)
-    logits_bytes = w.B * w.V * 4
-    print(json.dumps({
-        "read_floor_us": us_read, "read_floor_gbs": logits_bytes / us_read / 1e3,
-        "read_floor_frac_of_peak": logits_bytes / us_read / 1e3 / PEAK_HBM_GBS,
-        "workload": w.name, "logits_bytes": logits_bytes,
-        "steps": args.steps, "input_sets": n_sets,
-    }), flush=True)
 
 
 def cpu_baseline(w, seconds: float, threads: int = 1) -> dict:
@@ -161,9 +110,6 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
         return
-    if args.read_floor:
-        read_floor(args)
-        return
 
     import torch
 
@@ -175,8 +121,10 @@ def main():
     w = make_workload(args.config, B=args.batch)
     if args.top_k is not None:
         params = w.params.copy()
+        old_k = int(params["top_k"][0])
         params["top_k"] = args.top_k
         w.params = params
+        w.description = w.description.replace(f"top_k={old_k}", f"top_k={args.top_k} (overridden)")
     sampler = Sampler(0)
 
     # Device-resident input sets, rotated so each launch misses the MALL.
@@ -231,11 +179,18 @@ def main():
     bytes_per_launch = w.B * w.bytes_per_row()
     achieved = bytes_per_launch / (ms_per_step * 1e-3) / 1e9
 
+    # HBM traffic per launch comes from rocprofv3 counter runs (FETCH_SIZE and
+    # WRITE_SIZE, scaled by a copy of known size), recorded with the source
+    # hash of the library they measured: reported only for that build.
+    from scriptonait_amd.build import source_hash
+
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{w.name}.json"
     if tf.exists() and args.top_k is None and args.batch is None:
         try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+            rec = json.loads(tf.read_text())
+            if rec.get("source_hash") == source_hash():
+                traffic = rec.get("hbm_bytes_per_launch")
         except Exception:
             traffic = None
 

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LLMHIP_ABI_VERSION 2
+#define LLMHIP_ABI_VERSION 3
 
 enum {
   LLMHIP_OK = 0,
@@ -143,7 +143,8 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
  * (Generator::step with recent_tokens, crates/llm-core/src/generate.rs:
  * 157-165 and 178-182). For every row b with done[b] == 0 it samples from
  * the row's logits exactly as llmhip_sample_device does, with `recent` =
- * the last min(ring_len[b], window) tokens of the row's history, then
+ * the last min(ring_len[b] - hist_start[b], window) tokens of the row's
+ * history, then
  *   - at eos_id: sets done[b] = 1 (Generator::step returns None), and
  *   - otherwise: appends the token, ring[b*ring_cap + ring_len[b] %
  *     ring_cap] = id, ring_len[b] += 1 (Generator::advance).
@@ -156,16 +157,25 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
  *             prompt and sets ring_len
  *   ring_len  device [B] u32 in/out: tokens row b has seen so far
  *   done      device nullable [B] u32 in/out
+ *   hist_start device nullable [B] u32: the first token (counted from the
+ *             start of row b's history, as ring_len counts) still in the
+ *             row's model cache. recent_tokens reads the cache's tokens
+ *             (generate.rs:178-182), and a cache reset keeps only the last
+ *             context_len / 2 of them (maybe_reset_cache, generate.rs:
+ *             187-196): a caller whose window can exceed what a reset keeps
+ *             sets hist_start[b] = ring_len[b] - keep when it resets row b's
+ *             cache (before it appends the token that follows). Null: the
+ *             whole ring is in the cache.
  *   window    repetition_window (SamplingConfig, generate.rs:25-80), at
  *             most ring_cap
  * params is a host pointer, as in llmhip_sample_device; logits, allowed,
- * rng_state and out_ids are device pointers.
+ * rng_state and out_ids are device pointers. V must be at least 1.
  */
 int llmhip_decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
                        const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
-                       uint32_t* ring_len, uint32_t* done, size_t window, const uint8_t* allowed,
-                       size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
-                       void* stream);
+                       uint32_t* ring_len, uint32_t* done, const uint32_t* hist_start, size_t window,
+                       const uint8_t* allowed, size_t allowed_len, uint32_t eos_id, uint64_t* rng_state,
+                       uint32_t* out_ids, void* stream);
 
 /*
  * The allowed mask as bits, built on the device from a corpus's tokens
@@ -198,9 +208,46 @@ int llmhip_sample_device_bits(llmhip_ctx* ctx, const float* logits, size_t B, si
 /* llmhip_decode_step with the allowed mask as bits (see above). */
 int llmhip_decode_step_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
                             const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
-                            uint32_t* ring_len, uint32_t* done, size_t window, const uint32_t* allowed_bits,
-                            size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
-                            void* stream);
+                            uint32_t* ring_len, uint32_t* done, const uint32_t* hist_start, size_t window,
+                            const uint32_t* allowed_bits, size_t allowed_len, uint32_t eos_id,
+                            uint64_t* rng_state, uint32_t* out_ids, void* stream);
+
+/*
+ * Status of a context's stream-ordered calls (no reference counterpart: the
+ * reference's sampler cannot fail). The device entries above return once
+ * their kernels are enqueued, so a kernel that hits an internal limit (a
+ * wait between wavefronts that ran out of spins; a bug, never an input
+ * condition) records it in a device word instead. This call waits for
+ * `stream`, reads the words that the device entries' kernels set since the
+ * last call, and clears them. llmhip_sample_host keeps a word of its own,
+ * cleared at its start, and reports its own kernels' flags as its return
+ * status.
+ *   flags      LLMHIP_KSTATUS_* bits of device-entry calls (0: all well; the
+ *              ids of a flagged call are not trustworthy)
+ *   handovers  rows that the register or the full-vocabulary kernel handed
+ *              to the sorting path, in calls of any entry (a performance
+ *              figure: the ids are the reference's either way)
+ */
+#define LLMHIP_KSTATUS_SYNC_TIMEOUT 1u
+typedef struct llmhip_status {
+  uint32_t flags;
+  uint32_t handovers;
+} llmhip_status;
+int llmhip_ctx_status(llmhip_ctx* ctx, void* stream, llmhip_status* out);
+
+/*
+ * Test hooks (no reference counterpart), to exercise the error paths
+ * without a kernel fault or hang:
+ *   LLMHIP_DEBUG_SPIN_LIMIT  later calls on ctx bound each wait between
+ *                            wavefronts by `value` spins (0: the default,
+ *                            about 0.1 s); a wait that runs out flags
+ *                            LLMHIP_KSTATUS_SYNC_TIMEOUT and the kernel
+ *                            still finishes
+ *   LLMHIP_DEBUG_SET_FLAGS   ORs `value` into the device-entry flags
+ */
+#define LLMHIP_DEBUG_SPIN_LIMIT 1
+#define LLMHIP_DEBUG_SET_FLAGS 2
+int llmhip_ctx_debug(llmhip_ctx* ctx, int what, uint32_t value);
 
 #ifdef __cplusplus
 }

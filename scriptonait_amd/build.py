@@ -1,5 +1,4 @@
-"""Build step for the gfx950 sampler library (libllmhip_sampler.so) and the
-read-floor probe (libllmhip_probe.so).
+"""Build step for the gfx950 sampler library (libllmhip_sampler.so).
 
 Compiles the HIP sources under csrc/ with hipcc for gfx950 only, in-tree,
 so the built library travels with the source tree. Flags that matter for
@@ -27,11 +26,21 @@ CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libllmhip_sampler.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 SOURCES = ["sampler_kernels.hip", "sampler_api.hip"]
-# Measurement kernels (the streaming-read floor bench.py --read-floor reports);
-# not part of the sampler's ABI.
-PROBE_SOURCE = "read_probe.hip"
-PROBE_PATH = PKG_DIR / "libllmhip_probe.so"
 ARCH = "gfx950"
+
+
+def source_hash() -> str:
+    """SHA-256 (first 16 hex digits) over the library's sources and the
+    header: the identity of a build, which measured profile figures name so
+    that bench.py can tell whether they belong to the library it runs."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.hip")) + [PKG_DIR.parent / "include" / "llmhip_sampler.h"]
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def hipcc_path() -> str:
@@ -75,12 +84,6 @@ def build_library(verbose: bool = False) -> Path:
     os.replace(tmp, LIB_PATH)
     for o in objs:
         Path(o).unlink(missing_ok=True)
-    tmp = PROBE_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc, *compile_flags(), "-shared", "-o", str(tmp), str(CSRC / PROBE_SOURCE)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
-    os.replace(tmp, PROBE_PATH)
     return LIB_PATH
 
 

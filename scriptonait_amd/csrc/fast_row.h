@@ -182,16 +182,15 @@ __device__ __forceinline__ uint32_t lds_peek(const uint32_t* p) {
 
 // Wait until *ctr >= target. Every wave that counts toward a target signals
 // it unconditionally before it waits on anything, so the wait ends. The
-// spin is bounded all the same (about 0.1 s): should that ever run out (a
-// bug, not an input condition), the wave records it in the call's status
-// word and carries on, so the kernel still finishes and the host entry
-// reports the failure instead of the GPU hanging.
-constexpr uint32_t kSpinLimit = 1u << 20;
-__device__ __forceinline__ void lds_wait(const uint32_t* ctr, uint32_t target, uint32_t* status) {
+// spin is bounded all the same (a.spin_limit spins, about 0.1 s by
+// default): should that ever run out (a bug, not an input condition), the
+// wave records it in the call's status word and carries on, so the kernel
+// still finishes and the failure is reported instead of the GPU hanging.
+__device__ __forceinline__ void lds_wait(const uint32_t* ctr, uint32_t target, const SampleArgs& a) {
   uint32_t spins = 0;
   while (lds_peek(ctr) < target) {
-    if (++spins > kSpinLimit) {
-      if ((threadIdx.x & 63u) == 0u) atomicOr(status, kStatusSyncTimeout);
+    if (++spins > a.spin_limit) {
+      if ((threadIdx.x & 63u) == 0u) atomicOr(a.status, kStatusSyncTimeout);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -199,13 +198,26 @@ __device__ __forceinline__ void lds_wait(const uint32_t* ctr, uint32_t target, u
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Wait until *p != 0 and return that value (0 if the bounded spin ran out,
-// as in lds_wait).
-__device__ __forceinline__ uint32_t lds_wait_nonzero(const uint32_t* p, uint32_t* status) {
+// Publish v (nonzero) in *p unless a value is there already; returns the
+// value *p holds afterwards (the first one published wins).
+__device__ __forceinline__ uint32_t lds_publish(uint32_t* p, uint32_t v) {
+  uint32_t old = 0u;  // the value expected: nothing published yet
+  if ((threadIdx.x & 63u) == 0u)
+    __hip_atomic_compare_exchange_strong(p, &old, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  // On success old still holds 0; on failure it holds the value found.
+  old = readlane_u32(old, 0);
+  return old ? old : v;
+}
+
+// Wait until *p != 0 and return that value. Should the bounded spin run out
+// (as in lds_wait), the wave publishes `fallback` itself, so every wave of
+// the workgroup still reads one and the same value.
+__device__ __forceinline__ uint32_t lds_wait_nonzero(uint32_t* p, uint32_t fallback, const SampleArgs& a) {
   uint32_t spins = 0, v;
   while ((v = lds_peek(p)) == 0u) {
-    if (++spins > kSpinLimit) {
-      if ((threadIdx.x & 63u) == 0u) atomicOr(status, kStatusSyncTimeout);
+    if (++spins > a.spin_limit) {
+      if ((threadIdx.x & 63u) == 0u) atomicOr(a.status, kStatusSyncTimeout);
+      v = lds_publish(p, fallback);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -421,7 +433,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   asm volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.params), "s"(a.params_stride), "s"(a.hist),
                "s"(a.hist_offsets), "s"(a.slotmask), "s"(a.status), "s"(a.rng_state), "s"(a.out_ids),
                "s"(a.out_probs), "s"(a.out_kept), "s"(a.row_class_mask), "s"(a.ring), "s"(a.ring_len),
-               "s"(a.done), "s"(a.ring_cap), "s"(a.window));
+               "s"(a.done), "s"(a.ring_cap), "s"(a.window), "s"(a.hist_start), "s"(a.spin_limit));
   asm volatile("" ::"s"(a.shared.temperature), "s"(a.shared.top_k), "s"(a.shared.top_p), "s"(a.shared.min_p),
                "s"(a.shared.repetition_penalty), "s"(a.eos_id), "s"(a.allowed), "s"(a.allowed_len), "s"(a.B),
                "s"(a.scratch), "s"(a.scratch_row_words));
@@ -440,11 +452,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // which count in order with the row's loads: a scalar load would share its
   // counter with LDS operations, and every LDS wait before it returned
   // (behind the row) would wait for it.
-  // hv: lanes 0-1 read hist_offsets[b], [b+1] (CSR) or ring_len[b], done[b]
-  // (decode-step mode).
+  // hv: lanes 0-1 read hist_offsets[b], [b+1] (CSR), or lanes 0-2 read
+  // ring_len[b], done[b], hist_start[b] (decode-step mode).
   const bool ring = a.ring_cap != 0u;
   const bool has_hist = ring || (a.hist_offsets && a.hist);
-  const uint32_t* hvsrc = ring ? ((lane & 1u) && a.done ? a.done + b : a.ring_len + b)
+  const uint32_t l3 = lane & 3u;
+  const uint32_t* hvsrc = ring ? (l3 == 1u && a.done ? a.done + b : l3 == 2u && a.hist_start ? a.hist_start + b : a.ring_len + b)
                                : (has_hist ? a.hist_offsets + b + (lane & 1u) : a.slotmask);
   const uint32_t hv = *hvsrc;
   const uint32_t rv = reinterpret_cast<const uint32_t*>(a.rng_state + b)[lane & 1u];
@@ -485,7 +498,11 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   for (int c = NB0; c < NCH; ++c) load_chunk(c);
   __builtin_amdgcn_sched_barrier(0);
 
-  const uint32_t h0 = has_hist ? readlane_u32(hv, 0) : 0u, h1 = has_hist ? readlane_u32(hv, 1) : 0u;
+  const uint32_t hv0 = readlane_u32(hv, 0), hv1 = readlane_u32(hv, 1), hv2 = readlane_u32(hv, 2);
+  const uint32_t h0 = has_hist ? hv0 : 0u;
+  // CSR: hist_offsets[b + 1]; ring: the ring's tokens still in the cache.
+  const uint32_t h1 = ring ? (a.hist_start ? (hv0 > hv2 ? hv0 - hv2 : 0u) : hv0) : (has_hist ? hv1 : 0u);
+  const bool row_done = ring && a.done && hv1 != 0u;
   const uint32_t len_b = h0;  // ring length (decode-step mode)
   const uint64_t rng0 = ((uint64_t)readlane_u32(rv, 1) << 32) | readlane_u32(rv, 0);
   llmhip_params P = a.shared;
@@ -524,7 +541,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   const uint32_t cls = row_class(P, V);
   if (!(cls & a.row_class_mask)) return true;
   // Decode-step mode: a finished generation is skipped (no draw).
-  if (ring && a.done && h1 != 0u) {
+  if (row_done) {
     if (tid == 0) {
       a.out_ids[b] = a.eos_id;
       if (a.out_kept) a.out_kept[b] = 0u;
@@ -554,7 +571,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // flight at a time.
   auto count_history = [&](uint32_t part, uint32_t nparts) __attribute__((always_inline)) {
     if (use_pen) {
-      lds_wait(&L.misc[kSyncZero], kWaves, a.status);
+      lds_wait(&L.misc[kSyncZero], kWaves, a);
       const uint32_t stride = nparts * 64u;
       for (uint32_t j0 = part * 64u; j0 < H; j0 += 8u * stride) {
         uint32_t ids[8];
@@ -592,7 +609,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     count_history(wave, kWaves);
     uint32_t pmv = 0u;
     if (use_pen) {
-      lds_wait(&L.misc[kSyncHist], kWaves, a.status);
+      lds_wait(&L.misc[kSyncHist], kWaves, a);
       pmv = L.pm[tid];
     }
     fix_all(pmv);
@@ -652,7 +669,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
         const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, Q, false, lane), T, lane);
         // A bounded threshold key is above 0x007fffff (lower_past_ties), so
         // 1 is free to say "not bounded".
-        if (lane == 0) __hip_atomic_store(&L.misc[kTauState], tkey ? tkey : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        (void)lds_publish(&L.misc[kTauState], tkey ? tkey : 1u);
       }
     }
   }
@@ -665,7 +682,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   //    published threshold appends one entry (the chunk's 4 values and its
   //    position) to the wave's region: one compare per chunk, and for the
   //    chunks where some lane hits, one ballot offset and two LDS writes.
-  const uint32_t tau = lds_wait_nonzero(&L.misc[kTauState], a.status);
+  const uint32_t tau = lds_wait_nonzero(&L.misc[kTauState], 1u, a);
   if (tau <= 1u) return false;  // every wave read the same published state
   float tf = key2f(tau);
   LLMHIP_MARK(4);
@@ -736,7 +753,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
   };
   if (use_pen) {
-    lds_wait(&L.misc[kSyncHist], kTauWaves, a.status);
+    lds_wait(&L.misc[kSyncHist], kTauWaves, a);
     pmv = L.pm[tid];
   }
   settle();
@@ -757,17 +774,17 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     for (int e = 0; e < NCH * 4; ++e) tm = fmaxf(tm, x[e]);
     reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
+    lds_barrier();  // every wave has read the candidate count and overflow flag above
     if (tid == 0) {
       L.misc[kCandN] = 0u;
       L.misc[kOverflow] = 0u;
     }
-    lds_barrier();
     if (tm > -INFINITY) {
       const uint32_t k = f2key(tm);
       atomicAdd(&L.coarse[k >> 24], 1u);
       atomicAdd(&L.fine[k >> 20], 1u);
     }
-    lds_barrier();
+    lds_barrier();  // the histogram and the reset words, before the appends
     const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, K, true, lane), T, lane);
     if (tkey == 0u) return false;
     tf = key2f(tkey);

@@ -80,7 +80,8 @@ struct llmhip_ctx {
   DevBuf params;                 // per-row params copied from the host
   DevBuf zeros;                  // kBlock zero words: the fast path's "no mask" slot mask
   DevBuf slotmask;               // kBlock words: the allowed mask in the fast path's layout
-  DevBuf status;                 // one word of kStatus* bits set by the kernels (zero when all is well)
+  DevBuf status;                 // kStatusWords words: kernel flags (host / device calls) and the hand-over count
+  uint32_t spin_limit = kSpinLimit;  // bound of the kernels' waits between wavefronts
   // staging of the host entry
   DevBuf logits, hist, hoff, allowed, rng, ids, probs, kept;
 };
@@ -130,6 +131,7 @@ struct RingArgs {
   uint32_t* ring = nullptr;
   uint32_t* ring_len = nullptr;
   uint32_t* done = nullptr;
+  const uint32_t* hist_start = nullptr;
   uint32_t cap = 0;
   uint32_t window = 0;
 };
@@ -138,7 +140,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
             const llmhip_params* params_host, size_t params_stride, const llmhip_params* params_dev,
             const uint32_t* hist, const uint32_t* hist_offsets, const Mask& mask, uint32_t eos_id,
             uint64_t* rng_state, uint32_t* out_ids, float* out_probs, uint32_t* out_kept, hipStream_t s,
-            const RingArgs& ring = RingArgs()) {
+            bool host_call, const RingArgs& ring = RingArgs()) {
   if (V == 0) {
     // Empty logits: sample_with returns 0 without drawing (generate.rs:375-377).
     HIP_TRY(hipMemsetAsync(out_ids, 0, B * sizeof(uint32_t), s));
@@ -178,6 +180,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.ring = ring.ring;
   a.ring_len = ring.ring_len;
   a.done = ring.done;
+  a.hist_start = ring.hist_start;
   a.ring_cap = ring.cap;
   a.window = ring.window;
   a.allowed = mask.len ? mask.bytes : nullptr;
@@ -189,7 +192,9 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.out_probs = out_probs;
   a.out_kept = out_kept;
   a.slotmask = static_cast<const uint32_t*>(ctx->zeros.ptr);
-  a.status = static_cast<uint32_t*>(ctx->status.ptr);
+  a.status = static_cast<uint32_t*>(ctx->status.ptr) + (host_call ? kStatusHostWord : kStatusDeviceWord);
+  a.handovers = static_cast<uint32_t*>(ctx->status.ptr) + kStatusHandoverWord;
+  a.spin_limit = ctx->spin_limit;
   a.scratch = static_cast<uint32_t*>(ctx->scratch.ptr);
   a.scratch_row_words = row_words;
 
@@ -236,11 +241,13 @@ namespace {
 // One decode step (llmhip_decode_step and its bit-mask twin).
 int decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
                 const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
-                uint32_t* ring_len, uint32_t* done, size_t window, const Mask& mask, const void* mask_ptr,
-                uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids, void* stream) {
+                uint32_t* ring_len, uint32_t* done, const uint32_t* hist_start, size_t window, const Mask& mask,
+                const void* mask_ptr, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids, void* stream) {
   if (!ctx) return arg_fail("ctx is null");
   int st = validate(B, V, ld, logits, params, nullptr, nullptr, mask_ptr, mask.len, rng_state, out_ids);
   if (st || B == 0) return st;
+  // A generation over an empty vocabulary has no token to append.
+  if (V == 0) return arg_fail("V must be at least 1 for a decode step");
   if (!ring || !ring_len) return arg_fail("ring and ring_len are required");
   if (ring_cap == 0 || ring_cap > 0x7fffffffu) return arg_fail("ring_cap must be in 1 .. 2^31-1");
   if (window > ring_cap) return arg_fail("window must not exceed ring_cap");
@@ -254,10 +261,11 @@ int decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t
   r.ring = ring;
   r.ring_len = ring_len;
   r.done = done;
+  r.hist_start = hist_start;
   r.cap = (uint32_t)ring_cap;
   r.window = (uint32_t)window;
   return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, nullptr, nullptr, mask, eos_id, rng_state,
-                 out_ids, nullptr, nullptr, s, r);
+                 out_ids, nullptr, nullptr, s, false, r);
 }
 
 }  // namespace
@@ -303,10 +311,10 @@ int llmhip_ctx_create(int device, llmhip_ctx** out_ctx) {
     return hip_fail(e, "hipStreamCreateWithFlags");
   }
   int st = ctx->zeros.ensure(kBlock * sizeof(uint32_t));
-  if (st == LLMHIP_OK) st = ctx->status.ensure(sizeof(uint32_t));
+  if (st == LLMHIP_OK) st = ctx->status.ensure(kStatusWords * sizeof(uint32_t));
   if (st == LLMHIP_OK) {
     e = hipMemset(ctx->zeros.ptr, 0, kBlock * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(ctx->status.ptr, 0, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(ctx->status.ptr, 0, kStatusWords * sizeof(uint32_t));
     if (e != hipSuccess) st = hip_fail(e, "hipMemset");
   }
   if (st != LLMHIP_OK) {
@@ -353,7 +361,7 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
   m.bytes = allowed;
   m.len = allowed_len;
   return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state,
-                 out_ids, out_probs, out_kept, s);
+                 out_ids, out_probs, out_kept, s, false);
 }
 
 int llmhip_sample_device_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
@@ -376,7 +384,7 @@ int llmhip_sample_device_bits(llmhip_ctx* ctx, const float* logits, size_t B, si
   m.bits = allowed_bits;
   m.len = allowed_len;
   return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state,
-                 out_ids, out_probs, out_kept, s);
+                 out_ids, out_probs, out_kept, s, false);
 }
 
 int llmhip_seen_tokens(llmhip_ctx* ctx, const uint32_t* tokens, size_t n, size_t V, uint32_t* seen_bits,
@@ -405,6 +413,9 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
   Device d(ctx->device);
   if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
   hipStream_t s = ctx->stream;
+  uint32_t* host_word = static_cast<uint32_t*>(ctx->status.ptr) + kStatusHostWord;
+  // This call reports only what its own kernels flag.
+  HIP_TRY(hipMemsetAsync(host_word, 0, sizeof(uint32_t), s));
 
   // Rows are copied densely (ld = V on the device).
   const size_t nlog = B * V;
@@ -449,7 +460,7 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
                hist ? static_cast<const uint32_t*>(ctx->hoff.ptr) : nullptr, m,
                eos_id, static_cast<uint64_t*>(ctx->rng.ptr), static_cast<uint32_t*>(ctx->ids.ptr),
                out_probs ? static_cast<float*>(ctx->probs.ptr) : nullptr,
-               out_kept ? static_cast<uint32_t*>(ctx->kept.ptr) : nullptr, s);
+               out_kept ? static_cast<uint32_t*>(ctx->kept.ptr) : nullptr, s, true);
   if (st) {
     (void)hipStreamSynchronize(s);
     return st;
@@ -459,12 +470,10 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
   if (out_kept) HIP_TRY(hipMemcpyAsync(out_kept, ctx->kept.ptr, B * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   if (out_probs) HIP_TRY(hipMemcpyAsync(out_probs, ctx->probs.ptr, nlog * sizeof(float), hipMemcpyDeviceToHost, s));
   uint32_t kstatus = 0;
-  HIP_TRY(hipMemcpyAsync(&kstatus, ctx->status.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(&kstatus, host_word, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   if (kstatus) {
-    // A kernel hit an internal limit (its results are not trustworthy):
-    // report it and clear the word for the next call.
-    (void)hipMemset(ctx->status.ptr, 0, sizeof(uint32_t));
+    // A kernel hit an internal limit: its results are not trustworthy.
     g_last_error = "internal error: a workgroup sync wait timed out in the sampler kernel";
     return LLMHIP_ERR_HIP;
   }
@@ -473,26 +482,65 @@ int llmhip_sample_host(llmhip_ctx* ctx, const float* logits, size_t B, size_t V,
 
 int llmhip_decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
                        const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
-                       uint32_t* ring_len, uint32_t* done, size_t window, const uint8_t* allowed,
-                       size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
-                       void* stream) {
+                       uint32_t* ring_len, uint32_t* done, const uint32_t* hist_start, size_t window,
+                       const uint8_t* allowed, size_t allowed_len, uint32_t eos_id, uint64_t* rng_state,
+                       uint32_t* out_ids, void* stream) {
   Mask m;
   m.bytes = allowed;
   m.len = allowed_len;
-  return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, window, m,
-                     allowed, eos_id, rng_state, out_ids, stream);
+  return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, hist_start,
+                     window, m, allowed, eos_id, rng_state, out_ids, stream);
 }
 
 int llmhip_decode_step_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
                             const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
-                            uint32_t* ring_len, uint32_t* done, size_t window, const uint32_t* allowed_bits,
-                            size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
-                            void* stream) {
+                            uint32_t* ring_len, uint32_t* done, const uint32_t* hist_start, size_t window,
+                            const uint32_t* allowed_bits, size_t allowed_len, uint32_t eos_id,
+                            uint64_t* rng_state, uint32_t* out_ids, void* stream) {
   Mask m;
   m.bits = allowed_bits;
   m.len = allowed_len;
-  return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, window, m,
-                     allowed_bits, eos_id, rng_state, out_ids, stream);
+  return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, hist_start,
+                     window, m, allowed_bits, eos_id, rng_state, out_ids, stream);
+}
+
+int llmhip_ctx_status(llmhip_ctx* ctx, void* stream, llmhip_status* out) {
+  if (!ctx) return arg_fail("ctx is null");
+  if (!out) return arg_fail("out is null");
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t w[kStatusWords] = {0u, 0u, 0u, 0u};
+  HIP_TRY(hipMemcpyAsync(w, ctx->status.ptr, sizeof w, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  // The host entry's word stays: it is cleared by each host call itself.
+  uint32_t* dev = static_cast<uint32_t*>(ctx->status.ptr);
+  HIP_TRY(hipMemsetAsync(dev + kStatusDeviceWord, 0, 2 * sizeof(uint32_t), s));
+  HIP_TRY(hipStreamSynchronize(s));
+  out->flags = w[kStatusDeviceWord];
+  out->handovers = w[kStatusHandoverWord];
+  return LLMHIP_OK;
+}
+
+int llmhip_ctx_debug(llmhip_ctx* ctx, int what, uint32_t value) {
+  if (!ctx) return arg_fail("ctx is null");
+  switch (what) {
+    case LLMHIP_DEBUG_SPIN_LIMIT:
+      ctx->spin_limit = value ? value : kSpinLimit;
+      return LLMHIP_OK;
+    case LLMHIP_DEBUG_SET_FLAGS: {
+      Device d(ctx->device);
+      if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+      uint32_t w = 0u;
+      uint32_t* dev = static_cast<uint32_t*>(ctx->status.ptr) + kStatusDeviceWord;
+      HIP_TRY(hipMemcpy(&w, dev, sizeof w, hipMemcpyDeviceToHost));
+      w |= value;
+      HIP_TRY(hipMemcpy(dev, &w, sizeof w, hipMemcpyHostToDevice));
+      return LLMHIP_OK;
+    }
+    default:
+      return arg_fail("unknown debug request");
+  }
 }
 
 }  // extern "C"

@@ -64,18 +64,27 @@ struct SampleArgs {
   // or all zeros when there is no mask. 1024 words, always valid.
   const uint32_t* slotmask;
   // Decode-step mode (ring_cap > 0): row b's history is the last
-  // min(ring_len[b], window) tokens of the ring ring[b*ring_cap ..
-  // (b+1)*ring_cap) (hist == ring, hist_offsets == null); each result is
+  // min(ring_len[b] - hist_start[b], window) tokens of the ring ring[b*ring_cap
+  // .. (b+1)*ring_cap) (hist == ring, hist_offsets == null); each result is
   // appended to the ring (ring_len[b] += 1), or sets done[b] at eos_id, and
   // rows with done[b] != 0 are skipped.
   uint32_t* ring;
   uint32_t* ring_len;
   uint32_t* done;
+  // Decode-step mode, nullable: hist_start[b] is the first token (as a count
+  // since the start of the generation) still in row b's model cache; the
+  // history never reaches before it.
+  const uint32_t* hist_start;
   uint32_t ring_cap;
   uint32_t window;
   // Device word of kStatus* bits, set by a kernel that hit an internal
   // limit (zero after a correct call).
   uint32_t* status;
+  // Device counter of rows a kernel handed to the sorting path.
+  uint32_t* handovers;
+  // Spins before a wait between wavefronts gives up (kSpinLimit unless a
+  // test lowers it).
+  uint32_t spin_limit;
   uint32_t eos_id;
   uint64_t* rng_state;
   uint32_t* out_ids;
@@ -88,8 +97,10 @@ struct SampleArgs {
 
 // Row b's history (`recent`, generate.rs:343-352): the CSR slice
 // hist[hist_offsets[b] .. hist_offsets[b+1]), or in decode-step mode the
-// last H = min(ring_len[b], window) tokens of row b's ring (the penalty only
-// counts occurrences, so the ring's order does not matter).
+// last H = min(ring_len[b] - hist_start[b], window) tokens of row b's ring
+// (recent_tokens reads the model cache's tokens, generate.rs:178-182, which a
+// cache reset trims, :187-196; the penalty only counts occurrences, so the
+// ring's order does not matter).
 struct HistRow {
   const uint32_t* base;  // first id of the slice, or the row's ring
   uint32_t start;        // ring: slot of the oldest token in the window
@@ -102,12 +113,19 @@ struct HistRow {
   }
 };
 
-// v0, v1: hist_offsets[b], hist_offsets[b+1] (CSR) or ring_len[b] (ring).
+// Tokens of row b's ring still in its model cache (decode-step mode).
+__device__ __forceinline__ uint32_t ring_avail(const SampleArgs& a, uint32_t b, uint32_t len) {
+  const uint32_t s = a.hist_start ? a.hist_start[b] : 0u;
+  return len > s ? len - s : 0u;
+}
+
+// v0, v1: hist_offsets[b], hist_offsets[b+1] (CSR) or ring_len[b] and the
+// ring tokens still in the cache (ring).
 __device__ __forceinline__ HistRow hist_row(const SampleArgs& a, uint32_t b, uint32_t v0, uint32_t v1) {
   HistRow h{a.hist, 0u, 0u, 0u};
   if (a.ring_cap) {
     h.cap = a.ring_cap;
-    h.H = min(v0, a.window);
+    h.H = min(min(v0, v1), a.window);
     h.base = a.ring + (size_t)b * a.ring_cap;
     h.start = (v0 - h.H) % a.ring_cap;
   } else if (a.hist && a.hist_offsets && v1 > v0) {
@@ -140,6 +158,12 @@ enum RowClass : uint32_t {
 };
 
 constexpr uint32_t kStatusSyncTimeout = 1u;  // an LDS wait between waves ran out of spins
+constexpr uint32_t kSpinLimit = 1u << 20;    // default spins of a wait between waves (about 0.1 s)
+// Words of a context's status buffer.
+constexpr uint32_t kStatusHostWord = 0;      // flags of the current host-entry call
+constexpr uint32_t kStatusDeviceWord = 1;    // flags of device-entry calls since the last llmhip_ctx_status
+constexpr uint32_t kStatusHandoverWord = 2;  // rows handed to the sorting path since the last llmhip_ctx_status
+constexpr uint32_t kStatusWords = 4;
 
 constexpr uint32_t kBlock = 1024;
 constexpr uint32_t kWaves = kBlock / 64;

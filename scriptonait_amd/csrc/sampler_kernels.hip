@@ -158,6 +158,7 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   uint32_t h0 = 0, h1 = 0;
   if (a.ring_cap) {
     h0 = a.ring_len[b];
+    h1 = ring_avail(a, b, h0);
     // Decode-step mode: a finished generation is skipped (no draw).
     if (a.done && a.done[b]) {
       if (tid == 0) {
@@ -357,6 +358,7 @@ __global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
   if (!(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   const bool vec4 = (reinterpret_cast<uintptr_t>(a.logits) % 16u == 0u) && (a.ld % 4u == 0u);
   if (!vocab_row(a, b, L.v, vec4)) {
+    if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
     __syncthreads();
     general_row(a, b, L.gen);
   }
@@ -369,6 +371,7 @@ template <int NCH, bool VEC>
 __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   __shared__ FastLds<NCH> L;
   if (__builtin_expect(!fast_row<NCH, VEC>(a, L), 0)) {
+    if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
     __syncthreads();
     general_row(a, blockIdx.x, L.gen);
   }

@@ -368,7 +368,7 @@ __device__ __forceinline__ bool before(uint32_t ka, uint32_t ia, uint32_t kb, ui
 template <int NF, class Src>
 __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u, uint32_t keep_default, bool keep_count,
                                           VocabLds& L, const Src& src, const ListSrc& tl, bool tl_ok, uint32_t tl_k,
-                                          FoldRes (&res)[NF], uint32_t& keep_out, uint32_t* status) {
+                                          FoldRes (&res)[NF], uint32_t& keep_out, const SampleArgs& a) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t k0 = tid * 4u;
   const float S = fs[0].S, thr = fs[0].thr;  // the same terms for both folds
@@ -786,7 +786,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
   // integers, tie zones split at their ties, gathering zones 64 elements at a
   // time.
   if (wave == 0) {
-    lds_wait(&L.misc[kVSortDone], kWaves, status);  // every zone sorted, every segment summed
+    lds_wait(&L.misc[kVSortDone], kWaves, a);  // every zone sorted, every segment summed
     bool split_ready = nt == 0u;
     bool fail = false;
     uint32_t keep = keep_default;
@@ -874,7 +874,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
             uint32_t prev = 0;
             if (cf == kBTie) {
               if (!split_ready) {
-                lds_wait(&L.misc[kVSplitDone], kWaves - 1u, status);
+                lds_wait(&L.misc[kVSplitDone], kWaves - 1u, a);
                 split_ready = true;
               }
               const uint32_t t0 = readlane_u32(mT0, zi), tn = readlane_u32(mTn, zi);
@@ -1069,7 +1069,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   FoldSpec fs[1] = {{0.0f, 0.0f, 0.0f, INFINITY, false}};
   FoldRes r[1];
   uint32_t keep;
-  if (!run_folds<1>(fs, mx, 0.0f, V, false, L, src, lsrc, listed, kc, r, keep, a.status)) return false;
+  if (!run_folds<1>(fs, mx, 0.0f, V, false, L, src, lsrc, listed, kc, r, keep, a)) return false;
   const float S = r[0].F;
   if (!(S > 0.0f) || !isfinite(S)) return false;
 
@@ -1085,7 +1085,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
                       {0.0f, S, thr, INFINITY, true}};
     FoldRes rw[2];
     uint32_t keep;
-    if (!run_folds<2>(fw, mx, u, V, P.min_p > 0.0f, L, from, lsrc, listed, kc, rw, keep, a.status)) return false;
+    if (!run_folds<2>(fw, mx, u, V, P.min_p > 0.0f, L, from, lsrc, listed, kc, rw, keep, a)) return false;
     // The walk's stop, else order[keep - 1] (the cut); without either the
     // row is handed over.
     const bool walk_stop = rw[1].stop_pos != kNoPos, cut = rw[0].stop_pos != kNoPos;
@@ -1119,6 +1119,7 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   uint32_t h0 = 0, h1 = 0;
   if (a.ring_cap) {
     h0 = a.ring_len[b];
+    h1 = ring_avail(a, b, h0);
     if (a.done && a.done[b]) {
       if (tid == 0) {
         a.out_ids[b] = a.eos_id;

@@ -46,13 +46,22 @@ EXPORTED_SYMBOLS = (
     "llmhip_seen_tokens",
     "llmhip_sample_device_bits",
     "llmhip_decode_step_bits",
+    "llmhip_ctx_status",
+    "llmhip_ctx_debug",
 )
+KSTATUS_SYNC_TIMEOUT = 1
+DEBUG_SPIN_LIMIT = 1
+DEBUG_SET_FLAGS = 2
 
 
 class SamplerError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
         self.status = status
+
+
+class LlmhipStatus(ctypes.Structure):
+    _fields_ = [("flags", ctypes.c_uint32), ("handovers", ctypes.c_uint32)]
 
 
 class LlmhipParams(ctypes.Structure):
@@ -93,11 +102,16 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.llmhip_sample_device.restype = ctypes.c_int
     lib.llmhip_sample_device.argtypes = common + [vp]
     lib.llmhip_decode_step.restype = ctypes.c_int
-    lib.llmhip_decode_step.argtypes = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, sz, vp, sz, u32, vp, vp, vp]
+    decode = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, sz, vp, sz, u32, vp, vp, vp]
+    lib.llmhip_decode_step.argtypes = decode
     lib.llmhip_sample_device_bits.restype = ctypes.c_int
     lib.llmhip_sample_device_bits.argtypes = common + [vp]
     lib.llmhip_decode_step_bits.restype = ctypes.c_int
-    lib.llmhip_decode_step_bits.argtypes = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, sz, vp, sz, u32, vp, vp, vp]
+    lib.llmhip_decode_step_bits.argtypes = decode
+    lib.llmhip_ctx_status.restype = ctypes.c_int
+    lib.llmhip_ctx_status.argtypes = [vp, vp, ctypes.POINTER(LlmhipStatus)]
+    lib.llmhip_ctx_debug.restype = ctypes.c_int
+    lib.llmhip_ctx_debug.argtypes = [vp, ctypes.c_int, u32]
     lib.llmhip_seen_tokens.restype = ctypes.c_int
     lib.llmhip_seen_tokens.argtypes = [vp, vp, sz, sz, vp, vp]
     _lib = lib
@@ -290,12 +304,14 @@ class Sampler:
 
     def decode_step(self, logits, params: np.ndarray, ring, ring_len, done, window: int, rng_state, out_ids,
                     V: Optional[int] = None, allowed=None, eos_id: int = EOS, stream=None, allowed_bits=None,
-                    allowed_len: Optional[int] = None) -> None:
+                    allowed_len: Optional[int] = None, hist_start=None) -> None:
         """llmhip_decode_step on torch CUDA tensors: one Generator::step
         (generate.rs:157-165) for B generations whose history ring
         ([B, ring_cap] int32), lengths and done flags ([B] int32) and RNG
-        states ([B] int64 viewed as u64) live on the device. Enqueued on
-        `stream` (default: torch's current stream); does not synchronize."""
+        states ([B] int64 viewed as u64) live on the device; hist_start
+        ([B] int32, optional) is the first ring token still in each row's
+        model cache. Enqueued on `stream` (default: torch's current stream);
+        does not synchronize."""
         import torch
 
         B, ld = logits.shape
@@ -310,14 +326,27 @@ class Sampler:
                 raise ValueError("pass allowed or allowed_bits, not both")
             status = self.lib.llmhip_decode_step_bits(
                 self.ctx, dp(logits), B, V, ld, _ptr(params), stride, dp(ring), ring.shape[1], dp(ring_len),
-                dp(done), window, dp(allowed_bits), V if allowed_len is None else allowed_len, eos_id,
+                dp(done), dp(hist_start), window, dp(allowed_bits), V if allowed_len is None else allowed_len, eos_id,
                 dp(rng_state), dp(out_ids), stream.cuda_stream)
         else:
             status = self.lib.llmhip_decode_step(
                 self.ctx, dp(logits), B, V, ld, _ptr(params), stride, dp(ring), ring.shape[1], dp(ring_len),
-                dp(done), window, dp(allowed), 0 if allowed is None else allowed.numel(), eos_id,
+                dp(done), dp(hist_start), window, dp(allowed), 0 if allowed is None else allowed.numel(), eos_id,
                 dp(rng_state), dp(out_ids), stream.cuda_stream)
         _check(self.lib, status)
+
+
+    def status(self, stream=None) -> LlmhipStatus:
+        """llmhip_ctx_status: waits for `stream` (default: the null stream),
+        returns and clears the device-entry flags and the hand-over count."""
+        out = LlmhipStatus()
+        _check(self.lib, self.lib.llmhip_ctx_status(self.ctx, None if stream is None else stream.cuda_stream,
+                                                     ctypes.byref(out)))
+        return out
+
+    def debug(self, what: int, value: int) -> None:
+        """llmhip_ctx_debug (test hooks: DEBUG_SPIN_LIMIT, DEBUG_SET_FLAGS)."""
+        _check(self.lib, self.lib.llmhip_ctx_debug(self.ctx, what, value))
 
 
 _default: Optional[Sampler] = None

@@ -44,7 +44,7 @@ def test_params_struct_layout_matches_header():
 
 def test_version_and_status_strings():
     lib = smp.load_library()
-    assert lib.llmhip_abi_version() == 2
+    assert lib.llmhip_abi_version() == 3
     assert lib.llmhip_status_string(0) == b"ok"
     assert lib.llmhip_status_string(-1) == b"invalid argument"
     assert lib.llmhip_status_string(-2) == b"no HIP device"
@@ -66,6 +66,18 @@ def test_argument_validation_without_a_device():
     rc = lib.llmhip_ctx_create(0, None)
     assert rc == -1
     assert lib.llmhip_ctx_destroy(None) == 0
+    out = smp.LlmhipStatus()
+    assert lib.llmhip_ctx_status(None, None, ctypes.byref(out)) == -1
+    assert lib.llmhip_ctx_debug(None, smp.DEBUG_SPIN_LIMIT, 1) == -1
+
+
+def test_status_struct_layout_matches_header():
+    assert ctypes.sizeof(smp.LlmhipStatus) == 8
+    text = HEADER.read_text()
+    assert "uint32_t flags;" in text and "uint32_t handovers;" in text
+    assert re.search(r"#define LLMHIP_KSTATUS_SYNC_TIMEOUT 1u", text)
+    assert re.search(rf"#define LLMHIP_DEBUG_SPIN_LIMIT {smp.DEBUG_SPIN_LIMIT}\b", text)
+    assert re.search(rf"#define LLMHIP_DEBUG_SET_FLAGS {smp.DEBUG_SET_FLAGS}\b", text)
 
 
 def test_context_creation_reports_missing_device_or_succeeds():

@@ -7,6 +7,13 @@ appends the token, and ends the row at EOS. On the device the histories,
 lengths, done flags and RNG states stay in HBM across steps; on the CPU the
 same loop runs over Python lists with oracle.sample_batch. Every step's ids
 and the final rings, lengths, done flags and RNG states must match.
+
+With a context length, the CPU loop also resets each row's cache as
+Generator::advance does (maybe_reset_cache, generate.rs:187-196: at
+context_len tokens the cache keeps its last context_len / 2 before the new
+token is appended), so `recent` is the last window tokens of the cache, not
+of the whole history; the device loop is told where each row's cache starts
+through hist_start, as a caller would after resetting its model's cache.
 """
 import numpy as np
 import pytest
@@ -16,14 +23,14 @@ from scriptonait_amd.workloads import EOS_ID, make_params
 pytestmark = pytest.mark.gpu
 
 
-def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3):
+def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_len=None, max_prompt=300):
     import torch
 
     from oracle import oracle
 
     rs = np.random.default_rng(seed)
     dev = torch.device("cuda:0")
-    prompts = [rs.integers(0, V, size=int(rs.integers(1, 300))).astype(np.uint32) for _ in range(B)]
+    prompts = [rs.integers(0, V, size=int(rs.integers(1, max_prompt))).astype(np.uint32) for _ in range(B)]
     ring = np.zeros((B, cap), dtype=np.uint32)
     for b, pr in enumerate(prompts):
         for j, tok in enumerate(pr):
@@ -36,6 +43,9 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3):
     d_rng = torch.from_numpy(rng0.view(np.int64)).to(dev)
     d_ids = torch.zeros(B, dtype=torch.int32, device=dev)
     hist = [list(p) for p in prompts]
+    cache = [list(p) for p in prompts]  # the model cache's tokens (recent_tokens reads these)
+    d_start = torch.zeros(B, dtype=torch.int32, device=dev) if context_len else None
+    resets = 0
     done = np.zeros(B, dtype=bool)
     st = rng0.copy()
     for t in range(steps):
@@ -43,11 +53,12 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3):
         for b in range(B):  # some rows end at EOS along the way
             if (b + 3 * t) % 29 == 0:
                 logits[b, EOS_ID] = 60.0
-        sampler.decode_step(torch.from_numpy(logits).to(dev), prm, d_ring, d_len, d_done, window, d_rng, d_ids)
+        sampler.decode_step(torch.from_numpy(logits).to(dev), prm, d_ring, d_len, d_done, window, d_rng, d_ids,
+                            hist_start=d_start)
         live = np.nonzero(~done)[0]
         want = np.full(B, EOS_ID, dtype=np.uint32)
         if live.size:
-            recent = [np.array(hist[b][-window:], dtype=np.uint32) for b in live]
+            recent = [np.array(cache[b][-window:], dtype=np.uint32) for b in live]
             offs = np.concatenate([[0], np.cumsum([r.size for r in recent])]).astype(np.uint32)
             o = oracle.sample_batch(logits[live], prm, st[live], np.concatenate(recent), offs, V=V)
             want[live] = o.ids
@@ -56,10 +67,18 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3):
                 if o.ids[i] == EOS_ID:
                     done[b] = True
                 else:
+                    if context_len and len(cache[b]) >= context_len:
+                        cache[b] = cache[b][-max(context_len // 2, 1):]
+                        resets += 1
                     hist[b].append(int(o.ids[i]))
+                    cache[b].append(int(o.ids[i]))
+        if d_start is not None:
+            d_start.copy_(torch.tensor([len(hist[b]) - len(cache[b]) for b in range(B)], dtype=torch.int32))
         got = d_ids.cpu().numpy().view(np.uint32)
         assert np.array_equal(got, want), (t, np.nonzero(got != want)[0])
     assert done.any() and not done.all()
+    if context_len:
+        assert resets > 0
     assert np.array_equal(d_done.cpu().numpy() != 0, done)
     assert np.array_equal(d_rng.cpu().numpy().view(np.uint64), st)
     glen = d_len.cpu().numpy().view(np.uint32)
@@ -79,6 +98,33 @@ def test_decode_loop_top_k_path(sampler):
 def test_decode_loop_full_vocab_path(sampler):
     """top_k = 0 (the bucketed exact-fold path), with a strong penalty and a short window."""
     _run(sampler, 2048, make_params(1.0, 0, 0.9, 0.02, 1.8), window=16, cap=16)
+
+
+def test_decode_loop_cache_resets(sampler):
+    """A window (48) longer than what a cache reset keeps (context_len 64 -> 32
+    tokens): recent must come from the cache, so hist_start moves at each reset."""
+    _run(sampler, 32000, make_params(0.7, 64, 0.95, 0.05, 1.15), steps=40, window=48, cap=64, context_len=64,
+         max_prompt=60)
+
+
+def test_decode_loop_cache_resets_full_vocab(sampler):
+    _run(sampler, 2048, make_params(1.0, 0, 0.9, 0.02, 1.8), steps=40, window=48, cap=64, context_len=64,
+         max_prompt=60)
+
+
+def test_decode_step_rejects_an_empty_vocabulary(sampler):
+    import torch
+
+    from scriptonait_amd.sampler import SamplerError
+
+    dev = torch.device("cuda:0")
+    z = torch.zeros((4, 1), dtype=torch.float32, device=dev)
+    ring = torch.zeros((4, 8), dtype=torch.int32, device=dev)
+    ln = torch.zeros(4, dtype=torch.int32, device=dev)
+    rng = torch.zeros(4, dtype=torch.int64, device=dev)
+    ids = torch.zeros(4, dtype=torch.int32, device=dev)
+    with pytest.raises(SamplerError):
+        sampler.decode_step(z, make_params(0.7, 64, 0.95, 0.05, 1.15), ring, ln, None, 8, rng, ids, V=0)
 
 
 def test_decode_loop_greedy(sampler):

@@ -273,3 +273,29 @@ def test_per_row_params_match_shared():
     a = oracle.sample_batch(w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
     b = oracle.sample_batch(w.logits, per, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
     assert np.array_equal(a.ids, b.ids)
+
+
+def test_softmax_sum_is_a_left_fold_in_sorted_order():
+    """The softmax sum (generate.rs:374) adds the terms one at a time in
+    sorted order. Terms [t, t, 1] by id with 2^-25 < t < 2^-24 (t = expf(-17)):
+    in sorted order 1 + t rounds back to 1 (t is under half an ulp of 1), twice,
+    so S = 1 and p_max = 1 exactly, and the top-p cumulative reaches
+    top_p = 1 - 2^-24 at the first term (kept 1). An id-order, ascending or
+    pairwise sum adds t + t = 2t first, which is over half an ulp: S = 1 + 2^-23,
+    p_max = 1 - 2^-23 < top_p, and two terms are kept. The same holds with a
+    thousand small terms, where any order other than the sorted one moves S by
+    about 4e-5."""
+    t64 = np.exp(-17.0)
+    assert 2.0 ** -25 < t64 < 2.0 ** -24
+    top_p = np.float32(1.0) - np.float32(2.0 ** -24)
+    assert float(top_p) == 1.0 - 2.0 ** -24
+    for n_small in (2, 1000):
+        x = np.full(n_small + 1, -17.0, dtype=np.float32)
+        x[-1] = 0.0  # the maximum has the largest id: id order puts it last
+        prm = make_params(1.0, 0, float(top_p), 0.0, 1.0)
+        seeds = np.arange(16, dtype=np.uint64)
+        r = oracle.sample_batch(np.repeat(x[None, :], 16, axis=0), prm, seeds, want_probs=True)
+        assert np.all(r.ids == n_small)
+        assert np.all(r.kept == 1)
+        assert np.all(r.probs[:, -1] == np.float32(1.0))
+        assert np.all(r.probs[:, :-1] == 0.0)  # truncated by top-p: not among the kept terms
