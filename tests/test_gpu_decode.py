@@ -23,7 +23,8 @@ from scriptonait_amd.workloads import EOS_ID, make_params
 pytestmark = pytest.mark.gpu
 
 
-def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_len=None, max_prompt=300):
+def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_len=None, max_prompt=300,
+         eos_rows=1):
     import torch
 
     from oracle import oracle
@@ -50,7 +51,7 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_l
     st = rng0.copy()
     for t in range(steps):
         logits = (rs.standard_normal((B, V)) * 3.0).astype(np.float32)
-        for b in range(B):  # some rows end at EOS along the way
+        for b in range(0, B, eos_rows):  # some rows end at EOS along the way
             if (b + 3 * t) % 29 == 0:
                 logits[b, EOS_ID] = 60.0
         sampler.decode_step(torch.from_numpy(logits).to(dev), prm, d_ring, d_len, d_done, window, d_rng, d_ids,
@@ -104,12 +105,12 @@ def test_decode_loop_cache_resets(sampler):
     """A window (48) longer than what a cache reset keeps (context_len 64 -> 32
     tokens): recent must come from the cache, so hist_start moves at each reset."""
     _run(sampler, 32000, make_params(0.7, 64, 0.95, 0.05, 1.15), steps=40, window=48, cap=64, context_len=64,
-         max_prompt=60)
+         max_prompt=60, eos_rows=2)
 
 
 def test_decode_loop_cache_resets_full_vocab(sampler):
     _run(sampler, 2048, make_params(1.0, 0, 0.9, 0.02, 1.8), steps=40, window=48, cap=64, context_len=64,
-         max_prompt=60)
+         max_prompt=60, eos_rows=2)
 
 
 def test_decode_step_rejects_an_empty_vocabulary(sampler):
