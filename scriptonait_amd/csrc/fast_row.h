@@ -53,10 +53,6 @@
 
 namespace llmhip {
 
-// Top-k rows of the general path with K up to kSelCap are selected and
-// sorted in LDS; larger K sort the whole row in HBM scratch.
-constexpr uint32_t kSelCap = 4096;
-
 // LDS needed by the general path (about 53 KB).
 struct GenLds {
   uint32_t bins[256];

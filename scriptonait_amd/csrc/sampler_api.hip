@@ -127,6 +127,17 @@ struct Mask {
   size_t len = 0;
 };
 
+// Scratch words per row that a call may touch (row_scratch_words over its
+// rows, times Vp).
+size_t call_row_words(const llmhip_params* params, size_t B, size_t params_stride, size_t V) {
+  uint32_t w = kScratchSelWords;
+  const size_t n = params_stride ? B : 1;
+  for (size_t b = 0; b < n && w < kScratchSortWords; ++b)
+    w = std::max(w, row_scratch_words(params[b * params_stride], (uint32_t)V));
+  const size_t Vp = (V + kBlock - 1) / kBlock * kBlock;
+  return (size_t)w * Vp;
+}
+
 struct RingArgs {
   uint32_t* ring = nullptr;
   uint32_t* ring_len = nullptr;
@@ -162,8 +173,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
 
   // The fast kernel may hand a row to the general path, so scratch is
   // always sized for the batch.
-  const size_t Vp = (V + kBlock - 1) / kBlock * kBlock;
-  const size_t row_words = 5 * Vp;
+  const size_t row_words = call_row_words(params_host, B, params_stride, V);
   int st = ctx->scratch.ensure(B * row_words * sizeof(uint32_t));
   if (st) return st;
 

@@ -184,4 +184,21 @@ __host__ __device__ __forceinline__ uint32_t row_class(const llmhip_params& p, u
   return kClassFull;
 }
 
+// Top-k rows of the sorting path with K up to kSelCap are selected and
+// sorted in LDS; larger K (and full-vocabulary rows) sort the whole row in
+// HBM scratch.
+constexpr uint32_t kSelCap = 4096;
+
+// Scratch words per row, in units of Vp (V rounded up to kBlock), that a row
+// may touch: greedy rows and top-k rows that select in LDS use keys and
+// counts; a whole-row sort (and the full-vocabulary kernel's min-p list)
+// uses all five arrays.
+constexpr uint32_t kScratchSelWords = 2;
+constexpr uint32_t kScratchSortWords = 5;
+__host__ __device__ __forceinline__ uint32_t row_scratch_words(const llmhip_params& p, uint32_t V) {
+  if (p.temperature <= 0.0f) return kScratchSelWords;
+  if (p.top_k > 0 && p.top_k < V && p.top_k <= kSelCap) return kScratchSelWords;
+  return kScratchSortWords;
+}
+
 }  // namespace llmhip

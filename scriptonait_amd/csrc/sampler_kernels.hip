@@ -140,7 +140,10 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
 
 // ---------------------------------------------------------------------------
 // General path: one row, 1024 threads, scratch in HBM.
-// Scratch per row (Vp = V rounded up to 1024): keysA | idsA | keysB | idsB | cnt
+// Scratch per row (Vp = V rounded up to 1024): keysA | cnt | idsA | keysB |
+// idsB. Greedy rows and top-k rows that select in LDS touch only the first
+// two (kScratchSelWords), so a call without whole-row sorts needs 2*Vp words
+// per row; the sort needs all five (kScratchSortWords).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, GenLds& L) {
   const llmhip_params P = load_params(a, b);
@@ -148,10 +151,10 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   const uint32_t V = a.V;
   const uint32_t Vp = (V + kBlock - 1) / kBlock * kBlock;
   uint32_t* keysA = a.scratch + (size_t)b * a.scratch_row_words;
-  uint32_t* idsA = keysA + Vp;
+  uint32_t* cnt = keysA + Vp;
+  uint32_t* idsA = cnt + Vp;
   uint32_t* keysB = idsA + Vp;
   uint32_t* idsB = keysB + Vp;
-  uint32_t* cnt = idsB + Vp;
   const float* row = a.logits + (size_t)b * a.ld;
   if (tid < 32) L.exptab[tid] = exp2f_tab_lane(tid);
 
