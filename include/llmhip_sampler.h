@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LLMHIP_ABI_VERSION 3
+#define LLMHIP_ABI_VERSION 4
 
 enum {
   LLMHIP_OK = 0,
@@ -137,6 +137,37 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
                          const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
                          uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
                          uint32_t* out_kept, void* stream);
+
+/*
+ * llmhip_sample_device for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference: its sampler allocates a Vec
+ * per call (generate.rs:331, :364). Same arguments, meaning and results as
+ * llmhip_sample_device; the difference is where the device memory comes
+ * from. This call allocates nothing: the per-row parameters (params_stride
+ * != 0), the allowed mask's slot layout and the sorting path's per-row
+ * scratch go into one array of LLMHIP_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on, until the process ends. A call needs
+ *   ceil(((B - 1) * params_stride + 1) * 20 / 256) * 256   (params, if per row)
+ *   + 4096                                                 (mask layout)
+ *   + B * w * Vp * 4                                       (scratch)
+ * bytes, with Vp = V rounded up to 1024 and w = 2 when every row is greedy
+ * or has 0 < top_k <= 4096, top_k < V, else 5. A larger call returns
+ * LLMHIP_ERR_UNSUPPORTED (llmhip_last_error gives both sizes) and enqueues
+ * nothing. The B = 256, V = 32000 top-k batch needs 64 MiB.
+ * Every call on one GPU shares that GPU's array, whichever context makes it:
+ * calls that overlap on one GPU (on different streams, or from different
+ * threads) race and must be serialized by the caller. The kernels write
+ * every scratch word they read within the call, so the array's contents
+ * from an earlier call do not matter.
+ */
+#define LLMHIP_NOALLOC_SCRATCH_BYTES (96u << 20)
+int llmhip_sample_device_noalloc(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                                 const llmhip_params* params, size_t params_stride,
+                                 const uint32_t* hist, const uint32_t* hist_offsets,
+                                 const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
+                                 uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                                 uint32_t* out_kept, void* stream);
 
 /*
  * One decode step for B generations whose state lives in HBM

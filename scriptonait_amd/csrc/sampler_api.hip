@@ -7,9 +7,21 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "sampler_common.h"
+
+// Device memory of llmhip_sample_device_noalloc, for callers that cannot
+// allocate: each GPU the library runs on holds its own copy of this array
+// until the process ends. One call lays out, from the start: the per-row
+// parameters (when params_stride != 0), the allowed mask in the register
+// path's slot layout (kBlock words), and the per-row scratch of the sorting
+// path. Host code never passes `scratch` itself to a kernel or a copy (in
+// host code the name is a host-side stand-in, not a device address): it uses
+// the address hipGetSymbolAddress returns for the current device, looked up
+// once per device when the first context on that device is created.
+static __device__ __align__(256) uint32_t scratch[LLMHIP_NOALLOC_SCRATCH_BYTES / sizeof(uint32_t)];
 
 namespace llmhip {
 hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s);
@@ -82,11 +94,38 @@ struct llmhip_ctx {
   DevBuf slotmask;               // kBlock words: the allowed mask in the fast path's layout
   DevBuf status;                 // kStatusWords words: kernel flags (host / device calls) and the hand-over count
   uint32_t spin_limit = kSpinLimit;  // bound of the kernels' waits between wavefronts
+  uint32_t* noalloc = nullptr;   // this device's address of the file-scope `scratch` (null: lookup failed)
   // staging of the host entry
   DevBuf logits, hist, hoff, allowed, rng, ids, probs, kept;
 };
 
 namespace {
+
+// Device address of `scratch` on each device, looked up once per device.
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+uint32_t* g_noalloc_ptr[kMaxDevices];
+std::string g_noalloc_err[kMaxDevices];
+
+// The address of `scratch` on `device`, which must be the current device.
+// The first call per device looks it up; a failed lookup is kept (with its
+// message) and leaves only the no-alloc entry unusable.
+uint32_t* noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  if (!g_noalloc_ptr[device] && g_noalloc_err[device].empty()) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p) {
+      g_noalloc_ptr[device] = static_cast<uint32_t*>(p);
+    } else {
+      char buf[160];
+      snprintf(buf, sizeof buf, "hipGetSymbolAddress(scratch): %s (%d)", hipGetErrorString(e), (int)e);
+      g_noalloc_err[device] = buf;
+    }
+  }
+  return g_noalloc_ptr[device];
+}
 
 struct Device {
   int prev = -1;
@@ -127,6 +166,14 @@ struct Mask {
   size_t len = 0;
 };
 
+// Device memory one call works in: the context's buffers, grown as needed
+// (scratch == null), or fixed regions of the no-alloc array.
+struct Workspace {
+  uint32_t* scratch = nullptr;  // per-row scratch, scratch_bytes long
+  size_t scratch_bytes = 0;
+  uint32_t* slotmask = nullptr;  // kBlock words
+};
+
 // Scratch words per row that a call may touch (row_scratch_words over its
 // rows, times Vp).
 size_t call_row_words(const llmhip_params* params, size_t B, size_t params_stride, size_t V) {
@@ -151,7 +198,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
             const llmhip_params* params_host, size_t params_stride, const llmhip_params* params_dev,
             const uint32_t* hist, const uint32_t* hist_offsets, const Mask& mask, uint32_t eos_id,
             uint64_t* rng_state, uint32_t* out_ids, float* out_probs, uint32_t* out_kept, hipStream_t s,
-            bool host_call, const RingArgs& ring = RingArgs()) {
+            bool host_call, const RingArgs& ring = RingArgs(), const Workspace* ws = nullptr) {
   if (V == 0) {
     // Empty logits: sample_with returns 0 without drawing (generate.rs:375-377).
     HIP_TRY(hipMemsetAsync(out_ids, 0, B * sizeof(uint32_t), s));
@@ -174,8 +221,15 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   // The fast kernel may hand a row to the general path, so scratch is
   // always sized for the batch.
   const size_t row_words = call_row_words(params_host, B, params_stride, V);
-  int st = ctx->scratch.ensure(B * row_words * sizeof(uint32_t));
-  if (st) return st;
+  int st = LLMHIP_OK;
+  uint32_t* scr = nullptr;
+  if (ws) {
+    if (B * row_words * sizeof(uint32_t) > ws->scratch_bytes) return arg_fail("workspace too small for the call");
+    scr = ws->scratch;
+  } else {
+    if ((st = ctx->scratch.ensure(B * row_words * sizeof(uint32_t)))) return st;
+    scr = static_cast<uint32_t*>(ctx->scratch.ptr);
+  }
 
   SampleArgs a{};
   a.logits = logits;
@@ -205,7 +259,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.status = static_cast<uint32_t*>(ctx->status.ptr) + (host_call ? kStatusHostWord : kStatusDeviceWord);
   a.handovers = static_cast<uint32_t*>(ctx->status.ptr) + kStatusHandoverWord;
   a.spin_limit = ctx->spin_limit;
-  a.scratch = static_cast<uint32_t*>(ctx->scratch.ptr);
+  a.scratch = scr;
   a.scratch_row_words = row_words;
 
   if (out_probs) HIP_TRY(hipMemsetAsync(out_probs, 0, B * V * sizeof(float), s));
@@ -214,9 +268,13 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0) && (V % 4 == 0);
   if (fast_mask) {
     if (a.allowed || a.allowed_bits) {
-      if ((st = ctx->slotmask.ensure(kBlock * sizeof(uint32_t)))) return st;
-      HIP_TRY(launch_slotmask(a, static_cast<uint32_t*>(ctx->slotmask.ptr), s));
-      a.slotmask = static_cast<const uint32_t*>(ctx->slotmask.ptr);
+      uint32_t* sm = ws ? ws->slotmask : nullptr;
+      if (!sm) {
+        if ((st = ctx->slotmask.ensure(kBlock * sizeof(uint32_t)))) return st;
+        sm = static_cast<uint32_t*>(ctx->slotmask.ptr);
+      }
+      HIP_TRY(launch_slotmask(a, sm, s));
+      a.slotmask = sm;
     }
     a.row_class_mask = fast_mask;
     HIP_TRY(launch_fast(a, vec, s));
@@ -315,6 +373,7 @@ int llmhip_ctx_create(int device, llmhip_ctx** out_ctx) {
   if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
   llmhip_ctx* ctx = new llmhip_ctx();
   ctx->device = device;
+  ctx->noalloc = noalloc_scratch(device);
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;
@@ -372,6 +431,56 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
   m.len = allowed_len;
   return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state,
                  out_ids, out_probs, out_kept, s, false);
+}
+
+int llmhip_sample_device_noalloc(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                                 const llmhip_params* params, size_t params_stride,
+                                 const uint32_t* hist, const uint32_t* hist_offsets,
+                                 const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
+                                 uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
+                                 uint32_t* out_kept, void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  int st = validate(B, V, ld, logits, params, hist, hist_offsets, allowed, allowed_len, rng_state,
+                    out_ids);
+  if (st || B == 0) return st;
+  if (!ctx->noalloc) {
+    const int dev = ctx->device;
+    g_last_error = dev >= 0 && dev < kMaxDevices && !g_noalloc_err[dev].empty()
+                       ? g_noalloc_err[dev]
+                       : std::string("no-alloc scratch: no device address for this device");
+    return LLMHIP_ERR_HIP;
+  }
+  // The call's layout in the array: params | slot mask | per-row scratch.
+  const size_t pbytes =
+      params_stride ? (((B - 1) * params_stride + 1) * sizeof(llmhip_params) + 255u) / 256u * 256u : 0u;
+  const size_t mbytes = kBlock * sizeof(uint32_t);
+  const size_t sbytes = V ? B * call_row_words(params, B, params_stride, V) * sizeof(uint32_t) : 0u;
+  if (pbytes + mbytes + sbytes > (size_t)LLMHIP_NOALLOC_SCRATCH_BYTES) {
+    char buf[200];
+    snprintf(buf, sizeof buf, "no-alloc scratch: the call needs %zu bytes, the maximum is %zu",
+             pbytes + mbytes + sbytes, (size_t)LLMHIP_NOALLOC_SCRATCH_BYTES);
+    g_last_error = buf;
+    return LLMHIP_ERR_UNSUPPORTED;
+  }
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* base = reinterpret_cast<uint8_t*>(ctx->noalloc);
+  const llmhip_params* pdev = nullptr;
+  if (params_stride) {
+    HIP_TRY(hipMemcpyAsync(base, params, ((B - 1) * params_stride + 1) * sizeof(llmhip_params),
+                           hipMemcpyHostToDevice, s));
+    pdev = reinterpret_cast<const llmhip_params*>(base);
+  }
+  Workspace ws;
+  ws.slotmask = reinterpret_cast<uint32_t*>(base + pbytes);
+  ws.scratch = reinterpret_cast<uint32_t*>(base + pbytes + mbytes);
+  ws.scratch_bytes = (size_t)LLMHIP_NOALLOC_SCRATCH_BYTES - pbytes - mbytes;
+  Mask m;
+  m.bytes = allowed;
+  m.len = allowed_len;
+  return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state,
+                 out_ids, out_probs, out_kept, s, false, RingArgs(), &ws);
 }
 
 int llmhip_sample_device_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "llmhip_ctx_destroy",
     "llmhip_sample_host",
     "llmhip_sample_device",
+    "llmhip_sample_device_noalloc",
     "llmhip_decode_step",
     "llmhip_seen_tokens",
     "llmhip_sample_device_bits",
@@ -101,6 +102,8 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.llmhip_sample_host.argtypes = common
     lib.llmhip_sample_device.restype = ctypes.c_int
     lib.llmhip_sample_device.argtypes = common + [vp]
+    lib.llmhip_sample_device_noalloc.restype = ctypes.c_int
+    lib.llmhip_sample_device_noalloc.argtypes = common + [vp]
     lib.llmhip_decode_step.restype = ctypes.c_int
     decode = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, sz, vp, sz, u32, vp, vp, vp]
     lib.llmhip_decode_step.argtypes = decode
@@ -255,12 +258,14 @@ class Sampler:
     def sample_device(self, logits, params: np.ndarray, rng_state, out_ids, V: Optional[int] = None,
                       hist=None, hist_offsets=None, allowed=None, eos_id: int = EOS,
                       out_probs=None, out_kept=None, stream=None, allowed_bits=None,
-                      allowed_len: Optional[int] = None) -> None:
+                      allowed_len: Optional[int] = None, noalloc: bool = False) -> None:
         """llmhip_sample_device on torch CUDA tensors (logits [B, ld] f32,
         rng_state [B] int64 viewed as u64, out_ids [B] int32). Enqueued on
         `stream` (default: torch's current stream); does not synchronize.
         With allowed_bits (int32 words, as seen_tokens writes them; covering
-        allowed_len ids, default V) it calls llmhip_sample_device_bits."""
+        allowed_len ids, default V) it calls llmhip_sample_device_bits; with
+        noalloc, llmhip_sample_device_noalloc (the entry that allocates no
+        device memory)."""
         import torch
 
         B, ld = logits.shape
@@ -271,14 +276,15 @@ class Sampler:
             stream = torch.cuda.current_stream(logits.device)
         dp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         if allowed_bits is not None:
-            if allowed is not None:
-                raise ValueError("pass allowed or allowed_bits, not both")
+            if allowed is not None or noalloc:
+                raise ValueError("allowed_bits goes with neither allowed nor noalloc")
             status = self.lib.llmhip_sample_device_bits(
                 self.ctx, dp(logits), B, V, ld, _ptr(params), stride,
                 dp(hist), dp(hist_offsets), dp(allowed_bits), V if allowed_len is None else allowed_len,
                 eos_id, dp(rng_state), dp(out_ids), dp(out_probs), dp(out_kept), stream.cuda_stream)
         else:
-            status = self.lib.llmhip_sample_device(
+            entry = self.lib.llmhip_sample_device_noalloc if noalloc else self.lib.llmhip_sample_device
+            status = entry(
                 self.ctx, dp(logits), B, V, ld, _ptr(params), stride,
                 dp(hist), dp(hist_offsets), dp(allowed),
                 0 if allowed is None else allowed.numel(), eos_id,
