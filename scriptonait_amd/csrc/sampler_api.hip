@@ -213,9 +213,8 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   }
   const bool fast_ok = V <= kMaxFastV;
   const uint32_t fast_mask = fast_ok ? (classes & (kClassGreedy | kClassTopK)) : 0u;
-  // Full-vocabulary rows take the bucketed exact-fold kernel; it writes no
-  // out_probs, so a call that asks for them sorts those rows instead.
-  const uint32_t vocab_mask = out_probs ? 0u : (classes & kClassVocab);
+  // Full-vocabulary rows take the bucketed exact-fold kernel.
+  const uint32_t vocab_mask = classes & kClassVocab;
   const uint32_t general_mask = classes & ~fast_mask & ~vocab_mask;
 
   // The fast kernel may hand a row to the general path, so scratch is

@@ -247,6 +247,8 @@ struct StreamSrc {
   __device__ __forceinline__ void for_each(F&& f) const {
     for_each_part(f, 0u, kBlock);
   }
+  // Element i's post-temperature value.
+  __device__ __forceinline__ float value_at(uint32_t i) const { return wval(i, row[i]); }
   // Elements blk * 1024 .. blk * 1024 + 1023, by the calling wave.
   __device__ __forceinline__ uint32_t blocks() const { return (V + 1023u) / 1024u; }
   template <class F>
@@ -1096,6 +1098,27 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
       store_result(a, b, pick, len_b);
       a.rng_state[b] = st;
       if (a.out_kept) a.out_kept[b] = keep;
+    }
+    if (a.out_probs) {
+      // generate.rs:378-380 and 384-409: p_i = e_i / S over the kept prefix
+      // of the order, scattered by id into the row the caller has zeroed.
+      // The prefix ends at the top-p cut (the element at sorted position
+      // keep - 1, whose id the cumulative's replay found). Without a cut it
+      // is min-p's: p never increases along the order, so it holds exactly
+      // the elements with p >= thr. A prefix of one is order[0], which the
+      // walk then picks.
+      float* prow = a.out_probs + (size_t)b * V;
+      if (keep == 1u) {
+        if (tid == 0) prow[pick] = glibc_expf_tab(src.value_at(pick) - mx, L.exptab) / S;
+      } else {
+        const bool by_cut = cut;
+        const uint64_t cut_ord = by_cut ? cand_order(f2key(src.value_at(id_cut)), id_cut) : 0ull;
+        src.for_each([&](float w, uint32_t i) __attribute__((always_inline)) {
+          const float pi = glibc_expf_tab(w - mx, L.exptab) / S;
+          const bool kept = by_cut ? cand_order(f2key(w), i) >= cut_ord : pi >= thr;
+          if (kept && pi != 0.0f) prow[i] = pi;
+        });
+      }
     }
     return true;
   };

@@ -1,9 +1,13 @@
 """GPU: the full-vocabulary kernel (top_k == 0 or top_k >= V) against the oracle.
 
-These calls ask for no probabilities, which is what routes full-vocabulary
-rows to the bucketed exact-fold kernel (a call that wants out_probs sorts
-them instead). The bar is strict: every id, kept count and RNG state equals
-the oracle's; no tie allowance is used.
+Full-vocabulary rows go to the bucketed exact-fold kernel, which writes the
+post-truncation probabilities itself when they are asked for: every call
+here asks for them (except where a test says otherwise). The bar is strict:
+every id, kept count and RNG state equals the oracle's, with no tie
+allowance, and every probability equals the oracle's bit for bit (the stated
+contract is 1e-5 relative, which the test also checks). The hand-over count
+of llmhip_ctx_status says how many rows the kernel passed to the sorting
+path; configs 4 and 5 must pass none.
 """
 import numpy as np
 import pytest
@@ -14,9 +18,12 @@ from scriptonait_amd.workloads import PARAMS_DTYPE, make_params, make_workload
 pytestmark = pytest.mark.gpu
 
 
-def _both(sampler, logits, params, seeds, hist=None, offs=None, V=None, allowed=None):
-    g = sampler.sample_host(logits, params, seeds, hist, offs, allowed=allowed, V=V, want_probs=False)
-    o = oracle.sample_batch(logits, params, seeds, hist, offs, allowed=allowed, V=V, threads=8)
+def _both(sampler, logits, params, seeds, hist=None, offs=None, V=None, allowed=None, want_probs=True):
+    sampler.status()  # clears the hand-over count
+    g = sampler.sample_host(logits, params, seeds, hist, offs, allowed=allowed, V=V, want_probs=want_probs)
+    g.extra["handovers"] = sampler.status().handovers
+    o = oracle.sample_batch(logits, params, seeds, hist, offs, allowed=allowed, V=V, threads=8,
+                            want_probs=want_probs)
     return g, o
 
 
@@ -26,6 +33,13 @@ def _assert_same(g, o, label):
     bad = np.nonzero(g.kept != o.kept)[0]
     assert bad.size == 0, f"{label}: kept differs at rows {bad[:8]} gpu={g.kept[bad[:8]]} oracle={o.kept[bad[:8]]}"
     assert np.array_equal(g.rng_state, o.rng_state), f"{label}: rng state differs"
+    if g.probs is not None:
+        nz = o.probs != 0
+        bad = np.nonzero((g.probs != 0) != nz)[0]
+        assert bad.size == 0, f"{label}: kept sets differ at {bad[:8]}"
+        rel = np.abs(g.probs[nz] - o.probs[nz]) / np.abs(o.probs[nz])
+        assert rel.size == 0 or rel.max() <= 1e-5, f"{label}: probability off by {rel.max():.3g} relative"
+        assert np.array_equal(g.probs.view(np.uint32), o.probs.view(np.uint32)), f"{label}: probability bits differ"
 
 
 @pytest.mark.parametrize("cfg,B", [(4, 96), (5, 32)])
@@ -33,6 +47,26 @@ def test_full_vocab_configs(sampler, cfg, B):
     w = make_workload(cfg, B=B)
     g, o = _both(sampler, w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
     _assert_same(g, o, w.name)
+
+
+@pytest.mark.parametrize("cfg", [4, 5])
+def test_full_vocab_configs_full_batch(sampler, cfg):
+    """Configs 4 (B = 1024, V = 50257) and 5 (B = 512, V = 131072) whole:
+    every row is sampled by the bucketed kernel itself (no hand-over)."""
+    w = make_workload(cfg)
+    print(f"config {cfg}: B={w.B} V={w.V}", flush=True)
+    g, o = _both(sampler, w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
+    _assert_same(g, o, w.name)
+    assert g.extra["handovers"] == 0
+
+
+@pytest.mark.parametrize("cfg", [4, 5])
+def test_full_vocab_configs_without_probabilities(sampler, cfg):
+    """The timed form of the call (no out_probs) gives the same ids."""
+    w = make_workload(cfg, B=64)
+    g, o = _both(sampler, w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V, want_probs=False)
+    _assert_same(g, o, w.name)
+    assert g.extra["handovers"] == 0
 
 
 @pytest.mark.parametrize("cfg", [4, 5])
@@ -114,6 +148,7 @@ def test_rows_the_kernel_hands_to_the_sorting_path(sampler):
     seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
     g, o = _both(sampler, logits, prm, seeds, hist[: 2 * H], offs, V=V)
     _assert_same(g, o, "handed-over rows")
+    assert g.extra["handovers"] == 5  # rows 0-4; row 5 is an ordinary row
 
 
 def test_allowed_mask_full_vocab(sampler):
