@@ -18,6 +18,12 @@
 #include "sampler_common.h"
 #include "wave_ops.h"
 
+// Profiling hook: a profiling build defines LLMHIP_TAIL_MARK(i) (a
+// timestamp at step i of the register tail); empty otherwise.
+#ifndef LLMHIP_TAIL_MARK
+#define LLMHIP_TAIL_MARK(i)
+#endif
+
 namespace llmhip {
 
 // The same computation for n <= 4096 candidates, with the terms staged in
@@ -339,6 +345,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
                                                 uint64_t st_next, const uint64_t* tab, float* buf) {
   const uint32_t lane = lane_id();
   const bool act = lane < n;
+  LLMHIP_TAIL_MARK(0);
   const uint32_t k0 = readlane_u32(my_key, 0);
   const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
   const float e = act ? glibc_expf_tab(key2f(my_key) - mx, tab) : 0.0f;
@@ -369,6 +376,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
       for (int q = 0; q < 4; ++q) wc[q] = wn[q];
     }
   }
+  LLMHIP_TAIL_MARK(1);
   // generate.rs:375-377: degenerate exit, no draw.
   if (__builtin_expect(!(sum > 0.0f) || !isfinite(sum), 0)) {
     if (lane == 0) {
@@ -438,6 +446,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
     }
   }
 
+  LLMHIP_TAIL_MARK(2);
   if (__builtin_expect(!cert, 0)) {
     buf[lane] = p;
     // Terms 8k .. 8k+7, read from LDS per block (broadcast).
@@ -510,6 +519,7 @@ __device__ __forceinline__ void draw_tail_bcast(const SampleArgs& a, uint32_t b,
     }
   }
   const uint32_t id = readlane_u32(my_id, pick);
+  LLMHIP_TAIL_MARK(3);
   if (lane == 0) {
     store_result(a, b, id, len_b);
     a.rng_state[b] = st_next;

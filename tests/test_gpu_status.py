@@ -71,28 +71,51 @@ def test_status_is_read_once_and_stale_flags_do_not_fail_a_host_call(sampler):
 
 
 def test_timed_out_waits_are_reported_and_the_kernels_finish(sampler):
-    """One spin per wait: the waves that land before the threshold is
-    published give up waiting. The call must still finish (no hang, no
-    split workgroup) and report the timeout, through the host entry's
-    status and through llmhip_ctx_status for the device entry."""
-    w = make_workload(3, B=256)
+    """One spin per wait. The full-vocabulary kernel's replay wave always
+    waits for the other waves' tie split on config 4's rows, so that wait
+    runs out. The call must still finish (no hang, no split workgroup) and
+    report the timeout, through the host entry's status and through
+    llmhip_ctx_status for the device entry."""
+    from oracle import oracle
+
+    w = make_workload(4, B=64)
     sampler.status()
     sampler.debug(smp.DEBUG_SPIN_LIMIT, 1)
     try:
         with pytest.raises(smp.SamplerError) as e:
-            sampler.sample_host(w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
+            sampler.sample_host(w.logits, w.params, w.rng_seeds, V=w.V)
         assert e.value.status == -3
         _device_call(sampler, w)
         assert sampler.status().flags & smp.KSTATUS_SYNC_TIMEOUT
     finally:
         sampler.debug(smp.DEBUG_SPIN_LIMIT, 0)
     # Back to the default bound: clean again, and the ids are the oracle's.
-    from oracle import oracle
-
-    g = sampler.sample_host(w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
-    o = oracle.sample_batch(w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V, threads=8)
+    g = sampler.sample_host(w.logits, w.params, w.rng_seeds, V=w.V)
+    o = oracle.sample_batch(w.logits, w.params, w.rng_seeds, V=w.V, threads=8)
     assert np.array_equal(g.ids, o.ids)
     assert sampler.status().flags == 0
+
+
+def test_register_path_with_one_spin_per_wait(sampler):
+    """The register kernel's waits (for the threshold, for the history
+    counts) are usually over before a wave gets to them. With one spin per
+    wait a call either reports a timeout or returns the oracle's ids."""
+    from oracle import oracle
+
+    w = make_workload(3, B=256)
+    sampler.status()
+    sampler.debug(smp.DEBUG_SPIN_LIMIT, 1)
+    try:
+        try:
+            g = sampler.sample_host(w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V)
+        except smp.SamplerError as e:
+            assert e.status == -3
+        else:
+            o = oracle.sample_batch(w.logits, w.params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V, threads=8)
+            assert np.array_equal(g.ids, o.ids)
+    finally:
+        sampler.debug(smp.DEBUG_SPIN_LIMIT, 0)
+    sampler.status()
 
 
 def test_full_vocab_rows_report_their_handovers(sampler):
