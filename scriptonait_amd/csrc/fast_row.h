@@ -669,10 +669,11 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       }
     }
   }
-  // The history counts, by the same first kTauWaves waves: their ids are
-  // fetched while the other waves' rows are still landing, so the waves
-  // whose rows land last find the counts done.
-  if (arrive < kTauWaves) count_history(arrive, kTauWaves);
+  // The history counts, by the first kTauWaves - 1 waves (the last sample
+  // wave selects the threshold instead): their ids are fetched while the
+  // other waves' rows are still landing, and counted while they wait for
+  // the threshold, so the waves whose rows land last find the counts done.
+  if (arrive < kTauWaves - 1u) count_history(arrive, kTauWaves - 1u);
 
   // 3. The scan: every lane whose maximum over a chunk reaches the
   //    published threshold appends one entry (the chunk's 4 values and its
@@ -749,7 +750,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
   };
   if (use_pen) {
-    lds_wait(&L.misc[kSyncHist], kTauWaves, a);
+    lds_wait(&L.misc[kSyncHist], kTauWaves - 1u, a);
     pmv = L.pm[tid];
   }
   settle();
