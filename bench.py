@@ -44,6 +44,9 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=None, help="override B (not for the headline line)")
     ap.add_argument("--top-k", type=int, default=None,
                     help="override every row's top_k (not for the headline line)")
+    ap.add_argument("--tied-head", type=int, default=0, metavar="H",
+                    help="time llmhip_sample_tied_head_device (logits = hidden[B,H] @ embed[V,H]^T, then the "
+                         "sampler) on the workload's shape instead of the headline line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -98,6 +101,71 @@ def cpu_baseline(w, seconds: float, threads: int = 1) -> dict:
     }
 
 
+# Published MI355X figures: vector FP32 counts a packed pair of fused
+# multiply-adds as four flops. The head computes each product and sum as its
+# own binary32 operation (the reference's order), one lane op each, with no
+# fused or packed forms: at most a quarter of that rate.
+PEAK_FP32_TFLOPS = 157.3
+
+
+def bench_tied_head(args) -> None:
+    """Timing of the tied head plus the sampler: B rows of config `args.config`
+    (V and the sampling parameters), hidden rows N(0, 1) and embed N(0, 0.02^2).
+    The head's share is the entry's time minus the sampler's alone on the
+    same logits."""
+    import torch
+
+    from scriptonait_amd.sampler import Sampler
+    from scriptonait_amd.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload(args.config, B=args.batch)
+    H = args.tied_head
+    g = torch.Generator(device="cpu").manual_seed(7)
+    hidden = torch.randn((w.B, H), generator=g).to(dev)
+    embed = (0.02 * torch.randn((w.V, H), generator=g)).to(dev)
+    hs = torch.from_numpy(w.hist.view(np.int32)).to(dev) if w.hist is not None else None
+    offs = torch.from_numpy(w.hist_offsets.view(np.int32)).to(dev) if w.hist is not None else None
+    rng = torch.from_numpy(w.rng_seeds.view(np.int64)).to(dev)
+    ids = torch.empty(w.B, dtype=torch.int32, device=dev)
+    logits = torch.empty((w.B, w.V), dtype=torch.float32, device=dev)
+    sampler = Sampler(0)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, steps):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    steps = max(1, min(args.steps, 200))
+    both = timed(lambda: sampler.sample_tied_head_device(hidden, embed, w.params, rng, ids, hist=hs, hist_offsets=offs,
+                                                         out_logits=logits, stream=stream), steps)
+    alone = timed(lambda: sampler.sample_device(logits, w.params, rng, ids, V=w.V, hist=hs, hist_offsets=offs,
+                                                stream=stream), steps)
+    head_ms = both - alone
+    flops = 2.0 * w.B * w.V * H
+    tflops = flops / (head_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "tied head + sampler, us per step",
+        "value": both * 1e3, "unit": "us", "higher_is_better": False, "steps": steps, "warmup": args.warmup,
+        "config": {"workload": f"{w.name} with logits = hidden[{w.B},{H}] @ embed[{w.V},{H}]^T", "B": w.B, "V": w.V,
+                   "h": H},
+        "head_us": head_ms * 1e3, "sampler_us": alone * 1e3,
+        "roofline": {"bound": "valu", "achieved": tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / PEAK_FP32_TFLOPS, "traffic": None,
+                     "attainable_peak_exact_order": PEAK_FP32_TFLOPS / 4},
+        "dtype": "f32", "data": "synthetic (hidden N(0,1), embed N(0,0.02^2), torch seed 7)",
+    }), flush=True)
+    sampler.close()
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -109,6 +177,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.tied_head:
+        bench_tied_head(args)
         return
 
     import torch

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LLMHIP_ABI_VERSION 4
+#define LLMHIP_ABI_VERSION 5
 
 enum {
   LLMHIP_OK = 0,
@@ -168,6 +168,32 @@ int llmhip_sample_device_noalloc(llmhip_ctx* ctx, const float* logits, size_t B,
                                  const uint8_t* allowed, size_t allowed_len, uint32_t eos_id,
                                  uint64_t* rng_state, uint32_t* out_ids, float* out_probs,
                                  uint32_t* out_kept, void* stream);
+
+/*
+ * The tied output head and the sampler in one call, on device buffers:
+ * logits = hidden @ embed^T (crates/llm-core/src/model.rs:396-397,
+ * ops::linear_fwd(&final_normed, &weights.embed, 1, h, vocab), batched over
+ * B rows), then llmhip_sample_device on those logits. Every logit is the
+ * reference's dot product bit for bit (crates/llm-core/src/ops/linear.rs:
+ * 19-32: four accumulators over the chunks of 4, binary32 products and
+ * adds with no fused multiply-add, ((acc0 + acc1) + (acc2 + acc3)) + the
+ * remainder's fold), so the ids are those of sample_with on the CPU
+ * model's logits. Replaces the per-token logits read-back of
+ * crates/llm-gpu/src/model.rs:481-490.
+ *
+ *   hidden      device [B][ldh] f32: the final-normed hidden rows
+ *               (`final_normed`, one per generation)
+ *   embed       device [V][lde] f32: the embedding table, tied with the head
+ *   out_logits  nullable device [B][V] f32: receives the logits; null keeps
+ *               them in the context (they are consumed by the sampler)
+ * Every other argument is llmhip_sample_device's. Stream-ordered.
+ */
+int llmhip_sample_tied_head_device(llmhip_ctx* ctx, const float* hidden, size_t B, size_t h, size_t ldh,
+                                   const float* embed, size_t V, size_t lde, const llmhip_params* params,
+                                   size_t params_stride, const uint32_t* hist, const uint32_t* hist_offsets,
+                                   const uint8_t* allowed, size_t allowed_len, uint32_t eos_id, uint64_t* rng_state,
+                                   uint32_t* out_ids, float* out_probs, uint32_t* out_kept, float* out_logits,
+                                   void* stream);
 
 /*
  * One decode step for B generations whose state lives in HBM

@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY. Imported by tests/, by __graft_entry__.smoke() and
 by bench.py's cpu_baseline leg, always as the checker or the timed CPU
 baseline, never as the product path. The oracle restates
-crates/llm-core/src/generate.rs:325-420 and rng.rs:11-34 in C++
-(sampler_oracle.cpp).
+crates/llm-core/src/generate.rs:325-420, rng.rs:11-34 and
+ops/linear.rs:19-32, 110-125 in C++ (sampler_oracle.cpp).
 """
 from __future__ import annotations
 
@@ -49,6 +49,8 @@ def load() -> ctypes.CDLL:
     lib.oracle_next_f32.argtypes = [vp]
     lib.oracle_argmax.restype = u32
     lib.oracle_argmax.argtypes = [vp, sz]
+    lib.oracle_linear_fwd.restype = None
+    lib.oracle_linear_fwd.argtypes = [vp, vp, sz, sz, sz, vp, ctypes.c_int]
     lib.oracle_sample_batch.restype = ctypes.c_int
     lib.oracle_sample_batch.argtypes = [vp, sz, sz, sz, vp, sz, vp, vp, vp, sz, u32, vp, vp, vp, vp,
                                         vp, ctypes.c_int]
@@ -58,6 +60,22 @@ def load() -> ctypes.CDLL:
 
 def _ptr(a):
     return None if a is None else a.ctypes.data
+
+
+def linear_fwd(x: np.ndarray, w: np.ndarray, threads: int = 1) -> np.ndarray:
+    """crates/llm-core/src/ops/linear.rs:110-125: y = x @ w^T in the
+    reference's dot order (x [rows, in_dim], w [out_dim, in_dim], f32)."""
+    lib = load()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    rows, in_dim = x.shape
+    out_dim = w.shape[0]
+    assert w.shape[1] == in_dim
+    y = np.zeros((rows, out_dim), dtype=np.float32)
+    lib.oracle_linear_fwd(x.ctypes.data, w.ctypes.data, rows, in_dim, out_dim, y.ctypes.data, threads)
+    return y
 
 
 class OracleResult:

@@ -6,6 +6,8 @@
 // shipped library (scriptonait_amd/) links, loads or calls this file.
 //
 // Reference (all paths relative to the scriptonait repository):
+//   crates/llm-core/src/ops/linear.rs:19-32, 110-125  `dot`, `linear_fwd`
+//                                            (the tied output head's logits)
 //   crates/llm-core/src/rng.rs:11-34        SplitMix64 `Rng`
 //   crates/llm-core/src/ops/loss.rs:5-16     `argmax` (greedy tie-break)
 //   crates/llm-core/src/generate.rs:325-420  `sample_with`
@@ -31,7 +33,11 @@
 //   * closed forms (top_k = 1 and greedy give argmax; flat logits make the
 //     draw index floor(u * n)); brute force over all 2^24 draws for tiny
 //     rows (each id's share of draws equals its f32 probability mass);
-//   * an independent pure-Python restatement on small random rows.
+//   * an independent pure-Python restatement on small random rows;
+//   * linear_fwd: one-hot rows give the weight column exactly, small
+//     integers give the exact integer dot product, and rows built so that
+//     the four-accumulator order, a sequential fold and a pairwise sum give
+//     three different binary32 results pin the order.
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
@@ -49,6 +55,52 @@ typedef struct llmhip_params {
   float min_p;
   float repetition_penalty;
 } llmhip_params;
+
+// crates/llm-core/src/ops/linear.rs:19-32 (`dot`), as linear_fwd
+// (linear.rs:110-125, through dot_block :83-91) calls it for every (row,
+// output): four accumulators over the chunks of 4 (acc[k] += a[4j+k] *
+// b[4j+k], a separate binary32 multiply and add, in increasing j), then the
+// remainder's products as a left fold, then ((acc0 + acc1) + (acc2 + acc3))
+// + tail. Rust's f32 `Sum` starts its fold from a zero whose sign some
+// toolchains take as -0.0; the two starts differ only in the sign of an
+// all-zero tail, which leaves every nonzero result and every zero's value
+// unchanged. y is [rows][out_dim]; w is [out_dim][in_dim] (the tied head's
+// `embed`, model.rs:396-397).
+static float dot4(const float* a, const float* b, size_t n) {
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const size_t n4 = n / 4 * 4;
+  for (size_t j = 0; j < n4; j += 4) {
+    for (int k = 0; k < 4; ++k) {
+      const float prod = a[j + k] * b[j + k];
+      acc[k] = acc[k] + prod;
+    }
+  }
+  float tail = 0.0f;
+  for (size_t j = n4; j < n; ++j) {
+    const float prod = a[j] * b[j];
+    tail = tail + prod;
+  }
+  return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + tail;
+}
+
+void oracle_linear_fwd(const float* x, const float* w, size_t rows, size_t in_dim, size_t out_dim, float* y,
+                       int threads) {
+  auto work = [&](size_t r0, size_t r1) {
+    for (size_t r = r0; r < r1; ++r)
+      for (size_t o = 0; o < out_dim; ++o) y[r * out_dim + o] = dot4(x + r * in_dim, w + o * in_dim, in_dim);
+  };
+  if (threads <= 1 || rows < 2) {
+    work(0, rows);
+    return;
+  }
+  std::vector<std::thread> pool;
+  const size_t per = (rows + threads - 1) / threads;
+  for (int t = 0; t < threads; ++t) {
+    const size_t r0 = std::min(rows, t * per), r1 = std::min(rows, r0 + per);
+    if (r0 < r1) pool.emplace_back(work, r0, r1);
+  }
+  for (auto& th : pool) th.join();
+}
 
 // rng.rs:16-22
 uint64_t oracle_splitmix64_next(uint64_t* state) {

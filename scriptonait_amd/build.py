@@ -25,7 +25,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libllmhip_sampler.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["sampler_kernels.hip", "sampler_api.hip"]
+SOURCES = ["sampler_kernels.hip", "tied_head.hip", "sampler_api.hip"]
 ARCH = "gfx950"
 
 

@@ -29,6 +29,8 @@ hipError_t launch_general(const SampleArgs& a, hipStream_t s);
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s);
+hipError_t launch_tied_head(const float* hidden, uint64_t ldh, const float* embed, uint64_t lde, float* logits,
+                            uint64_t ldl, uint32_t B, uint32_t V, uint32_t h, hipStream_t s);
 }  // namespace llmhip
 
 using namespace llmhip;
@@ -93,6 +95,7 @@ struct llmhip_ctx {
   DevBuf zeros;                  // kBlock zero words: the fast path's "no mask" slot mask
   DevBuf slotmask;               // kBlock words: the allowed mask in the fast path's layout
   DevBuf status;                 // kStatusWords words: kernel flags (host / device calls) and the hand-over count
+  DevBuf head_logits;            // the tied head's logits when the caller does not take them
   uint32_t spin_limit = kSpinLimit;  // bound of the kernels' waits between wavefronts
   uint32_t* noalloc = nullptr;   // this device's address of the file-scope `scratch` (null: lookup failed)
   // staging of the host entry
@@ -401,8 +404,8 @@ int llmhip_ctx_destroy(llmhip_ctx* ctx) {
   Device d(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   (void)hipDeviceSynchronize();
-  for (DevBuf* b : {&ctx->scratch, &ctx->params, &ctx->zeros, &ctx->slotmask, &ctx->status, &ctx->logits, &ctx->hist,
-                    &ctx->hoff, &ctx->allowed, &ctx->rng, &ctx->ids, &ctx->probs, &ctx->kept})
+  for (DevBuf* b : {&ctx->scratch, &ctx->params, &ctx->zeros, &ctx->slotmask, &ctx->status, &ctx->head_logits,
+                    &ctx->logits, &ctx->hist, &ctx->hoff, &ctx->allowed, &ctx->rng, &ctx->ids, &ctx->probs, &ctx->kept})
     b->release();
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -480,6 +483,45 @@ int llmhip_sample_device_noalloc(llmhip_ctx* ctx, const float* logits, size_t B,
   m.len = allowed_len;
   return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state,
                  out_ids, out_probs, out_kept, s, false, RingArgs(), &ws);
+}
+
+int llmhip_sample_tied_head_device(llmhip_ctx* ctx, const float* hidden, size_t B, size_t h, size_t ldh,
+                                   const float* embed, size_t V, size_t lde, const llmhip_params* params,
+                                   size_t params_stride, const uint32_t* hist, const uint32_t* hist_offsets,
+                                   const uint8_t* allowed, size_t allowed_len, uint32_t eos_id, uint64_t* rng_state,
+                                   uint32_t* out_ids, float* out_probs, uint32_t* out_kept, float* out_logits,
+                                   void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  if (B == 0) return LLMHIP_OK;
+  if (h > 0x7fffffffu) return arg_fail("h must be below 2^31");
+  if (V > 0 && h > 0 && (!hidden || !embed)) return arg_fail("hidden and embed are required");
+  if (ldh < h || lde < h) return arg_fail("ldh and lde must be at least h");
+  if (V > 0x7fffffffu || B > 0x7fffffffu) return arg_fail("B and V must be below 2^31");
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // The logits: the caller's [B][V] buffer, or the context's, with rows
+  // padded to a multiple of 4 floats so the sampler reads them 16 bytes at
+  // a time.
+  float* lg = out_logits;
+  size_t ldl = V;
+  if (!lg && V > 0) {
+    ldl = (V + 3) / 4 * 4;
+    int st = ctx->head_logits.ensure(B * ldl * sizeof(float));
+    if (st) return st;
+    lg = static_cast<float*>(ctx->head_logits.ptr);
+  }
+  int st = validate(B, V, ldl, lg, params, hist, hist_offsets, allowed, allowed_len, rng_state, out_ids);
+  if (st) return st;
+  if (V > 0) HIP_TRY(launch_tied_head(hidden, ldh, embed, lde, lg, ldl, (uint32_t)B, (uint32_t)V, (uint32_t)h, s));
+  const llmhip_params* pdev = nullptr;
+  st = copy_params(ctx, params, B, params_stride, &pdev, s);
+  if (st) return st;
+  Mask m;
+  m.bytes = allowed;
+  m.len = allowed_len;
+  return enqueue(ctx, lg, B, V, ldl, params, params_stride, pdev, hist, hist_offsets, m, eos_id, rng_state, out_ids,
+                 out_probs, out_kept, s, false);
 }
 
 int llmhip_sample_device_bits(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,

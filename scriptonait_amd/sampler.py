@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "llmhip_sample_host",
     "llmhip_sample_device",
     "llmhip_sample_device_noalloc",
+    "llmhip_sample_tied_head_device",
     "llmhip_decode_step",
     "llmhip_seen_tokens",
     "llmhip_sample_device_bits",
@@ -104,6 +105,9 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.llmhip_sample_device.argtypes = common + [vp]
     lib.llmhip_sample_device_noalloc.restype = ctypes.c_int
     lib.llmhip_sample_device_noalloc.argtypes = common + [vp]
+    lib.llmhip_sample_tied_head_device.restype = ctypes.c_int
+    lib.llmhip_sample_tied_head_device.argtypes = [vp, vp, sz, sz, sz, vp, sz, sz, vp, sz, vp, vp, vp, sz, u32, vp, vp,
+                                                   vp, vp, vp, vp]
     lib.llmhip_decode_step.restype = ctypes.c_int
     decode = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, sz, vp, sz, u32, vp, vp, vp]
     lib.llmhip_decode_step.argtypes = decode
@@ -289,6 +293,30 @@ class Sampler:
                 dp(hist), dp(hist_offsets), dp(allowed),
                 0 if allowed is None else allowed.numel(), eos_id,
                 dp(rng_state), dp(out_ids), dp(out_probs), dp(out_kept), stream.cuda_stream)
+        _check(self.lib, status)
+
+    def sample_tied_head_device(self, hidden, embed, params: np.ndarray, rng_state, out_ids, hist=None,
+                                hist_offsets=None, allowed=None, eos_id: int = EOS, out_probs=None, out_kept=None,
+                                out_logits=None, stream=None) -> None:
+        """llmhip_sample_tied_head_device on torch CUDA tensors: logits =
+        hidden [B, h] @ embed [V, h]^T in the reference's dot order, then the
+        sampler on them. out_logits ([B, V] float32) receives the logits if
+        given. Enqueued on `stream` (default: torch's current stream)."""
+        import torch
+
+        B, h = hidden.shape
+        V = embed.shape[0]
+        if embed.shape[1] != h:
+            raise ValueError("embed must be [V, h]")
+        params = np.ascontiguousarray(params, dtype=PARAMS_DTYPE)
+        stride = 0 if params.shape[0] == 1 else 1
+        if stream is None:
+            stream = torch.cuda.current_stream(hidden.device)
+        dp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        status = self.lib.llmhip_sample_tied_head_device(
+            self.ctx, dp(hidden), B, h, hidden.stride(0), dp(embed), V, embed.stride(0), _ptr(params), stride,
+            dp(hist), dp(hist_offsets), dp(allowed), 0 if allowed is None else allowed.numel(), eos_id,
+            dp(rng_state), dp(out_ids), dp(out_probs), dp(out_kept), dp(out_logits), stream.cuda_stream)
         _check(self.lib, status)
 
     def seen_tokens(self, tokens, V: int, out_bits=None, stream=None):
