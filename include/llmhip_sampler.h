@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LLMHIP_ABI_VERSION 5
+#define LLMHIP_ABI_VERSION 6
 
 enum {
   LLMHIP_OK = 0,
@@ -291,6 +291,44 @@ typedef struct llmhip_status {
   uint32_t handovers;
 } llmhip_status;
 int llmhip_ctx_status(llmhip_ctx* ctx, void* stream, llmhip_status* out);
+
+/*
+ * Reader of scriptonait's checkpoint files ("SCCK", crates/llm-core/src/
+ * checkpoint.rs:11-24), so a real model's embedding table can feed
+ * llmhip_sample_tied_head_device. Host-side, no device work.
+ *
+ * llmhip_scck_parse checks `bytes` as Checkpoint::from_bytes does
+ * (checkpoint.rs:192-262: magic, version 2 to 4, ModelConfig::validate, the
+ * weight dtype, the tokenizer blob, the vocabulary-size consistency check,
+ * the weight length) and fills `out`. Fields a version lacks read as the
+ * reference's "not set" defaults (tokens_seen 0 before v3; planned_steps 0
+ * and plateau_scale 1.0 before v4). A file the reference rejects returns
+ * LLMHIP_ERR_INVALID_ARGUMENT, with the reason in llmhip_last_error.
+ *
+ * llmhip_scck_read_params widens `count` parameters, starting at parameter
+ * `first` in ModelWeights::tensors() order (model.rs:75-82: embed
+ * [vocab_size][hidden_dim] is parameters 0 .. vocab_size * hidden_dim,
+ * final_norm_gain the last hidden_dim), to f32 in `out` (host memory). bf16
+ * files widen as from_bf16 does (crates/llm-core/src/bf16.rs:22-25).
+ */
+typedef struct llmhip_scck_info {
+  uint32_t version;
+  uint32_t num_layers, hidden_dim, num_heads, num_kv_heads, context_len, local_window, vocab_size;
+  float rope_theta;
+  uint32_t use_ple;
+  uint64_t step;
+  uint64_t tokens_seen;
+  uint32_t planned_steps;
+  float plateau_scale;
+  uint32_t weight_dtype; /* 0 = f32, 1 = bf16 */
+  uint32_t num_merges;   /* the tokenizer's merges: vocab_size = 264 + num_merges */
+  uint64_t tokenizer_offset, tokenizer_bytes;
+  uint64_t weights_offset, weights_bytes;
+  uint64_t param_count;
+} llmhip_scck_info;
+int llmhip_scck_parse(const uint8_t* bytes, size_t len, llmhip_scck_info* out);
+int llmhip_scck_read_params(const uint8_t* bytes, size_t len, const llmhip_scck_info* info, uint64_t first,
+                            uint64_t count, float* out);
 
 /*
  * Test hooks (no reference counterpart), to exercise the error paths

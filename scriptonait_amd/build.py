@@ -25,7 +25,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libllmhip_sampler.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["sampler_kernels.hip", "tied_head.hip", "sampler_api.hip"]
+SOURCES = ["sampler_kernels.hip", "tied_head.hip", "sampler_api.hip", "scck_reader.cpp"]
 ARCH = "gfx950"
 
 
@@ -36,7 +36,8 @@ def source_hash() -> str:
     import hashlib
 
     h = hashlib.sha256()
-    files = sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.hip")) + [PKG_DIR.parent / "include" / "llmhip_sampler.h"]
+    files = (sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+             + [PKG_DIR.parent / "include" / "llmhip_sampler.h"])
     for f in files:
         h.update(f.name.encode())
         h.update(f.read_bytes())

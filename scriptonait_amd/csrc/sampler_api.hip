@@ -39,6 +39,15 @@ namespace {
 
 thread_local std::string g_last_error;
 
+}  // namespace
+
+namespace llmhip {
+// The text llmhip_last_error returns, set by code outside this file.
+void set_last_error(const std::string& what) { g_last_error = what; }
+}  // namespace llmhip
+
+namespace {
+
 int hip_fail(hipError_t e, const char* what) {
   char buf[256];
   snprintf(buf, sizeof buf, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);

@@ -50,6 +50,8 @@ EXPORTED_SYMBOLS = (
     "llmhip_decode_step_bits",
     "llmhip_ctx_status",
     "llmhip_ctx_debug",
+    "llmhip_scck_parse",
+    "llmhip_scck_read_params",
 )
 KSTATUS_SYNC_TIMEOUT = 1
 DEBUG_SPIN_LIMIT = 1
