@@ -25,7 +25,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libllmhip_sampler.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["sampler_kernels.hip", "tied_head.hip", "sampler_api.hip", "scck_reader.cpp"]
+SOURCES = ["sampler_kernels.hip", "fast_counts.hip", "tied_head.hip", "sampler_api.hip", "scck_reader.cpp"]
 ARCH = "gfx950"
 
 
@@ -68,15 +68,21 @@ def compile_flags() -> list[str]:
 
 def build_library(verbose: bool = False) -> Path:
     """Compile every HIP source and link the shared library. Always rebuilds."""
+    from concurrent.futures import ThreadPoolExecutor
+
     hipcc = hipcc_path()
-    objs = []
+    cmds, objs = [], []
     for src in SOURCES:
         obj = CSRC / (Path(src).stem + ".o")
-        cmd = [hipcc, *compile_flags(), "-c", str(CSRC / src), "-o", str(obj)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
+        cmds.append([hipcc, *compile_flags(), "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
+    if verbose:
+        for cmd in cmds:
+            print(" ".join(cmd), flush=True)
+    # The sources compile independently; the two kernel files dominate.
+    with ThreadPoolExecutor(max_workers=min(len(cmds), 4)) as pool:
+        for r in list(pool.map(lambda c: subprocess.run(c, check=True), cmds)):
+            pass
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs]
     if verbose:

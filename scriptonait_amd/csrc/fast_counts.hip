@@ -1,0 +1,12 @@
+// The register-path kernels for decode steps with a count table
+// (llmhip_decode_step_counts): the same kernel as the other calls, compiled
+// with the table's reads and updates in place of the history walk.
+#include "fast_kernel.h"
+
+namespace llmhip {
+
+hipError_t launch_fast_counts(const SampleArgs& a, bool vec, hipStream_t s) {
+  return launch_fast_mode<true>(a, vec, s);
+}
+
+}  // namespace llmhip

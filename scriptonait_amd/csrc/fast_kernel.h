@@ -1,0 +1,57 @@
+// The register-path kernel and its launch, templated on count-table mode:
+// decode steps with a count table run their own instantiations (compiled
+// in fast_counts.hip), so the other calls carry none of that code.
+#pragma once
+#include "fast_row.h"
+#include "general_row.h"
+#include "sampler_common.h"
+
+namespace llmhip {
+
+template <int NCH, bool VEC, bool GREEDY, bool CMODE>
+__global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
+  __shared__ FastLds<NCH> L;
+  if (__builtin_expect(!fast_row<NCH, VEC, GREEDY, CMODE>(a, L), 0)) {
+    if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
+    __syncthreads();
+    general_row(a, blockIdx.x, L.gen, true);
+  }
+}
+
+// One launch per row class present: greedy rows and top-k rows run in
+// kernels compiled apart, so neither carries the other's registers.
+template <int NCH, bool CMODE>
+hipError_t launch_fast_nch(const SampleArgs& a0, bool vec, hipStream_t s) {
+  SampleArgs a = a0;
+  if (a0.row_class_mask & kClassGreedy) {
+    a.row_class_mask = kClassGreedy;
+    if (vec) {
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, true, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, true, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (a0.row_class_mask & kClassTopK) {
+    a.row_class_mask = kClassTopK;
+    if (vec) {
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+    }
+  }
+  return hipGetLastError();
+}
+
+template <bool CMODE>
+hipError_t launch_fast_mode(const SampleArgs& a, bool vec, hipStream_t s) {
+  switch (fast_nch(a.V)) {
+    case 1: return launch_fast_nch<1, CMODE>(a, vec, s);
+    case 2: return launch_fast_nch<2, CMODE>(a, vec, s);
+    case 4: return launch_fast_nch<4, CMODE>(a, vec, s);
+    default: return launch_fast_nch<8, CMODE>(a, vec, s);
+  }
+}
+
+}  // namespace llmhip

@@ -19,9 +19,10 @@
 //     in a two-level key histogram; the 8th selects the threshold (about
 //     1.6K of the row's values expected at or above it, scaled from the half
 //     of the row those waves hold) and publishes it in LDS.
-//  3. the same 8 waves count the history ids: u16 multiplicities and
+//  3. the first 7 of them count the history ids: u16 multiplicities and
 //     per-owner masks of penalized slots, integer LDS atomics whose result
-//     does not depend on order.
+//     does not depend on order (in count-table mode the first wave slides
+//     the row's table in HBM instead).
 //  4. each chunk whose maximum reaches the threshold is compared value by
 //     value; hits go to the wave's LDS region.
 //  5. the wave settles its hits (mask, penalty m times in sequence,
@@ -71,6 +72,8 @@ constexpr uint32_t kCoarseBins = 256;             // key bits 31..24
 constexpr uint32_t kFineBins = 4096;              // key bits 31..20
 constexpr uint32_t kTauWaves = 8;                 // waves whose maxima form the threshold sample
 constexpr uint32_t kSpecNum = 8, kSpecDen = 5;    // the threshold aims at ~(kSpecNum/kSpecDen)*K values
+constexpr uint32_t kSpecMaxK = 384;               // larger K: the scan entries would overflow; proven threshold
+constexpr uint32_t kRefineCount = 16;             // a fine bin holding more keys is split once more
 
 // misc[] slots
 constexpr int kSyncSample = 0;  // waves whose sample is in the histogram
@@ -81,6 +84,11 @@ constexpr int kTauState = 4;    // 0: not yet, 1: row not bounded here, else the
 constexpr int kArrive = 6;   // waves whose row has landed, in arrival order
 constexpr int kSampled = 7;  // row positions held by the sample waves
 constexpr int kSyncZero = 8; // waves whose share of the count table is zeroed
+constexpr int kGreedyMax = 9; // greedy rows: key of the row's largest value known without a penalty
+constexpr int kCandN2 = 10;    // candidates of the second speculative pass
+constexpr int kOverflow2 = 11; // some wave's region overflowed in it
+constexpr int kTau2 = 12;      // its threshold key (1: no second pass)
+constexpr int kTau0 = 13;      // the proven threshold key (1: not bounded here)
 
 template <int NCH>
 struct FastLds {
@@ -92,7 +100,7 @@ struct FastLds {
   __attribute__((aligned(16))) uint32_t coarse[kCoarseBins];
   __attribute__((aligned(16))) uint32_t fine[kFineBins];
   float4 ent[kWaves * kEntries];     // scan entries: a lane's 4 values of a chunk with a hit
-  uint32_t etag[kWaves * kEntries];  // chunk position | hit mask << 24 | chunk << 28
+  __attribute__((aligned(16))) uint32_t etag[kWaves * kEntries];  // chunk position | chunk << 28
   __attribute__((aligned(16))) uint64_t ord[kFastCand];  // settled order keys; then the tail's terms
   uint32_t skey[kMaxFastK];  // sorted top-K: post-temperature key
   uint32_t sid[kMaxFastK];   //               id
@@ -281,19 +289,21 @@ __device__ __forceinline__ uint64_t exp2f_tab_lane(uint32_t lane) {
   return v;
 }
 
-// The Q-th largest key counted in the two-level histogram (coarse: key bits
-// 31..24, fine: bits 31..20), as a key threshold. exact: the lower edge of
-// the fine bin holding it, so at least Q counted keys lie at or above the
-// result. Otherwise an estimate inside that bin, taking its keys as evenly
-// spread. Returns 0 when fewer than Q keys were counted. Wave-local.
-__device__ __forceinline__ uint32_t hist_select(const uint32_t* coarse, const uint32_t* fine, uint32_t Q,
-                                                bool exact, uint32_t lane) {
+// Where the Q-th largest key counted in the two-level histogram (coarse:
+// key bits 31..24, fine: bits 31..20) lies: lo, the lower edge of the fine
+// bin holding it (0 when fewer than Q keys were counted), cnt, that bin's
+// count, and need (1..cnt), its rank inside the bin. Wave-local.
+struct HistPos {
+  uint32_t lo, cnt, need;
+};
+__device__ __forceinline__ HistPos hist_locate(const uint32_t* coarse, const uint32_t* fine, uint32_t Q,
+                                               uint32_t lane) {
   // Lane l holds coarse bins 255-4l .. 252-4l (w, z, y, x: descending).
   const uint4 q = reinterpret_cast<const uint4*>(coarse)[63u - lane];
   const uint32_t lt = q.x + q.y + q.z + q.w;
   const uint32_t ci = wave_incl_scan(lt);
   const uint64_t lm = __ballot(Q <= ci);
-  if (!lm) return 0u;
+  if (!lm) return HistPos{0u, 0u, 0u};
   const uint32_t l = (uint32_t)__ffsll((unsigned long long)lm) - 1u;
   uint32_t need = Q - (readlane_u32(ci, l) - readlane_u32(lt, l));
   const uint32_t cw = readlane_u32(q.w, l), cz = readlane_u32(q.z, l), cy = readlane_u32(q.y, l);
@@ -315,12 +325,20 @@ __device__ __forceinline__ uint32_t hist_select(const uint32_t* coarse, const ui
   const uint32_t fi = wave_incl_scan(fc);
   const uint64_t fm = __ballot(lane < 16u && need <= fi);
   const uint32_t fl = (uint32_t)__ffsll((unsigned long long)fm) - 1u;
-  const uint32_t lo = (cb * 16u + 15u - fl) << 20;
-  if (exact) return lo;
   const uint32_t cnt = readlane_u32(fc, fl);
-  const uint32_t need2 = need - (readlane_u32(fi, fl) - cnt);  // 1..cnt
-  // need2 <= cnt <= 1024, so need2 << 20 fits in 32 bits.
-  return lo + (1u << 20) - (need2 << 20) / (cnt + 1u);
+  return HistPos{(cb * 16u + 15u - fl) << 20, cnt, need - (readlane_u32(fi, fl) - cnt)};
+}
+
+// The Q-th largest key counted in the histogram, as a key threshold. exact:
+// the lower edge of the fine bin holding it, so at least Q counted keys lie
+// at or above the result. Otherwise an estimate inside that bin, taking its
+// keys as evenly spread. Returns 0 when fewer than Q keys were counted.
+__device__ __forceinline__ uint32_t hist_select(const uint32_t* coarse, const uint32_t* fine, uint32_t Q,
+                                                bool exact, uint32_t lane) {
+  const HistPos h = hist_locate(coarse, fine, Q, lane);
+  if (exact || h.lo == 0u) return h.lo;
+  // need <= cnt <= 1024, so need << 20 fits in 32 bits.
+  return h.lo + (1u << 20) - (h.need << 20) / (h.cnt + 1u);
 }
 
 // Lower a raw-value key threshold past every key whose value divided by T
@@ -413,7 +431,11 @@ __device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint32_t n, uint32_t 
 // One row on the register path. Returns false (uniformly across the
 // workgroup, before writing any output) when the row needs the general
 // path.
-template <int NCH, bool VEC>
+// GREEDY: the launch takes the greedy rows (temperature <= 0) only, else
+// the top-k rows only; each variant is compiled without the other's code.
+// CMODE: a decode step with a count table (a.ring and a.counts set); the
+// other calls run variants compiled without the table's code.
+template <int NCH, bool VEC, bool GREEDY, bool CMODE>
 __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   static_assert(NCH * 4 <= 32, "slot masks are 32 bits");
   typedef float f4v __attribute__((ext_vector_type(4)));
@@ -448,12 +470,17 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // which count in order with the row's loads: a scalar load would share its
   // counter with LDS operations, and every LDS wait before it returned
   // (behind the row) would wait for it.
-  // hv: lanes 0-1 read hist_offsets[b], [b+1] (CSR), or lanes 0-2 read
-  // ring_len[b], done[b], hist_start[b] (decode-step mode).
+  // hv: lanes 0-1 read hist_offsets[b], [b+1] (CSR), or lanes 0-4 read
+  // ring_len[b], done[b], hist_start[b], counted[2b], counted[2b+1]
+  // (decode-step mode; the last two with a count table).
   const bool ring = a.ring_cap != 0u;
   const bool has_hist = ring || (a.hist_offsets && a.hist);
-  const uint32_t l3 = lane & 3u;
-  const uint32_t* hvsrc = ring ? (l3 == 1u && a.done ? a.done + b : l3 == 2u && a.hist_start ? a.hist_start + b : a.ring_len + b)
+  constexpr bool cmode = CMODE;  // multiplicities from the count table
+  const uint32_t l7 = lane & 7u;
+  const uint32_t* hvsrc = ring ? (l7 == 1u && a.done ? a.done + b
+                                  : l7 == 2u && a.hist_start ? a.hist_start + b
+                                  : (l7 == 3u || l7 == 4u) && cmode ? a.counted + 2u * b + (l7 - 3u)
+                                  : a.ring_len + b)
                                : (has_hist ? a.hist_offsets + b + (lane & 1u) : a.slotmask);
   const uint32_t hv = *hvsrc;
   const uint32_t rv = reinterpret_cast<const uint32_t*>(a.rng_state + b)[lane & 1u];
@@ -495,6 +522,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   __builtin_amdgcn_sched_barrier(0);
 
   const uint32_t hv0 = readlane_u32(hv, 0), hv1 = readlane_u32(hv, 1), hv2 = readlane_u32(hv, 2);
+  const uint32_t hv3 = readlane_u32(hv, 3), hv4 = readlane_u32(hv, 4);
   const uint32_t h0 = has_hist ? hv0 : 0u;
   // CSR: hist_offsets[b + 1]; ring: the ring's tokens still in the cache.
   const uint32_t h1 = ring ? (a.hist_start ? (hv0 > hv2 ? hv0 - hv2 : 0u) : hv0) : (has_hist ? hv1 : 0u);
@@ -544,14 +572,36 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
     return true;
   }
-  if (__builtin_expect(H >= 65536u, 0)) return false;  // a u16 multiplicity could overflow
-  const bool greedy = cls == kClassGreedy;
+  // The count table's change for this step (every later return hands the
+  // row over with the table done). A rebuild takes the whole workgroup (it
+  // waits for the row's loads; it happens on a generation's first step and
+  // after a cache reset); a slide is made below by the first wave to land.
+  const CountsPlan cplan = cmode ? counts_plan(a, hv3, hv4, len_b, hr.H) : CountsPlan{0u, 0u, 0u, 0u, false};
+  if (cmode && cplan.rebuild) {
+    counts_rebuild(a, b, cplan);  // ends published, past a barrier
+    if (wave == 0) lds_signal(&L.misc[kSyncHist]);
+  }
+  // Rows handed over from here on have had their count table moved (the
+  // sorting path does not move it again).
+  auto slide_before_handover = [&]() __attribute__((always_inline)) {
+    if (cmode && !cplan.rebuild && wave == 0) counts_slide(a, b, cplan);
+  };
+  if (__builtin_expect(H >= 65536u, 0)) {  // a u16 multiplicity could overflow
+    slide_before_handover();
+    return false;
+  }
   // A penalty below 1 (or NaN) can raise a value above the raw one, so the
   // selection on raw values below does not bound such rows.
-  if (!greedy && use_pen && !(rp >= 1.0f)) return false;
+  if (!GREEDY && use_pen && !(rp >= 1.0f)) {
+    slide_before_handover();
+    return false;
+  }
   const uint32_t K = P.top_k;  // 0 < K < V, K <= kMaxFastK unless greedy (row class)
 
+  // Multiplicity of position p in the window. Positions past V (padding
+  // slots) have none, and the table holds no word for them.
   auto count_of = [&](uint32_t p) __attribute__((always_inline)) {
+    if (cmode) return p < V ? counts_at(a, b, p) : 0u;
     return (L.cnt[p >> 1] >> ((p & 1u) << 4)) & 0xffffu;
   };
   auto add_hist = [&](uint32_t id) __attribute__((always_inline)) {
@@ -597,18 +647,82 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       }
     }
   };
+  // Count-table mode: this thread's slots whose id is in the window (after
+  // the step's change is published). A chunk's four ids are two table
+  // words; positions past V have none.
+  auto table_bits = [&]() __attribute__((always_inline)) {
+    const uint32_t* row = counts_row(a, b);
+    constexpr int G = NCH < 4 ? NCH : 4;  // chunks whose words are in flight together
+    uint32_t bits = 0u;
+#pragma unroll
+    for (int c0 = 0; c0 < NCH; c0 += G) {
+      uint32_t wd[2 * G];
+#pragma unroll
+      for (int c = 0; c < G; ++c) {
+        const uint32_t p0 = chunk_pos<NCH>((uint32_t)(c0 + c), wave, lane);
+        wd[2 * c] = p0 < V ? __hip_atomic_load(&row[p0 >> 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        wd[2 * c + 1] =
+            p0 + 2u < V ? __hip_atomic_load(&row[(p0 >> 1) + 1u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      }
+#pragma unroll
+      for (int e = 0; e < G * 4; ++e) {
+        const uint32_t p = chunk_pos<NCH>((uint32_t)(c0 + (e >> 2)), wave, lane) + (uint32_t)(e & 3);
+        const uint32_t m = (wd[e >> 1] >> ((e & 1) << 4)) & 0xffffu;
+        if (m != 0u && p < V) bits |= 1u << (4 * c0 + e);
+      }
+    }
+    return bits;
+  };
+  // With rp >= 1 a penalty only lowers a value (v / rp for v > 0, v * rp
+  // otherwise), and a slot outside the history (or masked) has its final
+  // value already. So `known`, the thread's maximum over those slots, is a
+  // lower bound on its final maximum that needs no penalty.
+  auto known_max = [&](uint32_t pmv) __attribute__((always_inline)) {
+    float kv = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < NCH * 4; ++e)
+      if ((((pmv | mkbits) >> e) & 1u) == 0u) kv = fmaxf(kv, x[e]);
+    return kv;
+  };
 
-  if (__builtin_expect(greedy, 0)) {
+  if constexpr (GREEDY) {
     // ops/loss.rs:6-16 over the masked, penalized row (before temperature).
 #pragma unroll
     for (int c = 0; c < NCH; ++c) prep(c);
-    count_history(wave, kWaves);
     uint32_t pmv = 0u;
-    if (use_pen) {
-      lds_wait(&L.misc[kSyncHist], kWaves, a);
-      pmv = L.pm[tid];
+    if (cmode) {
+      // The table names the penalized slots once the step's change is in.
+      if (!cplan.rebuild && wave == 0) {
+        counts_slide(a, b, cplan);
+        counts_publish();
+        lds_signal(&L.misc[kSyncHist]);
+      }
+      lds_wait(&L.misc[kSyncHist], 1u, a);
+      if (use_pen) pmv = table_bits();
+    } else {
+      count_history(wave, kWaves);
+      if (use_pen) {
+        lds_wait(&L.misc[kSyncHist], kWaves, a);
+        pmv = L.pm[tid];
+      }
     }
-    fix_all(pmv);
+    if (use_pen && rp >= 1.0f) {
+      // The row's largest known value M0 bounds the winner from below: a
+      // history slot whose raw value is below M0 can neither win nor tie
+      // (a tie goes to the lower position), so only the others are
+      // penalized; the rest keep their raw values, which lose all the same.
+      const uint32_t kk = wave_max_u32(f2key(known_max(pmv)));
+      if (lane == 0u) atomicMax(&L.misc[kGreedyMax], kk);
+      lds_barrier();
+      const float m0 = key2f(L.misc[kGreedyMax]);
+      uint32_t need = 0u;
+#pragma unroll
+      for (int e = 0; e < NCH * 4; ++e)
+        if (x[e] >= m0) need |= 1u << e;
+      fix_all(pmv & need);
+    } else {
+      fix_all(pmv);
+    }
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
 #pragma unroll
@@ -641,6 +755,12 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   }
   LLMHIP_MARK(2);
 
+  // The sample position the speculative threshold takes: the target
+  // (kSpecNum/kSpecDen)*K scaled to the positions the sample holds.
+  auto spec_q = [&]() __attribute__((always_inline)) {
+    const uint64_t sampled = L.misc[kSampled];
+    return (uint32_t)(((uint64_t)kSpecNum * K * sampled + (uint64_t)kSpecDen * V - 1u) / ((uint64_t)kSpecDen * V)) + 2u;
+  };
   // 2. The first kTauWaves waves to get here put their sample maxima in the
   //    histogram, and the last of them selects the speculative threshold:
   //    the Q-th largest sampled maximum, with Q scaled from the target
@@ -659,10 +779,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       if (lds_signal(&L.misc[kSyncSample]) == kTauWaves - 1u) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         LLMHIP_MARK(3);
-        const uint64_t sampled = L.misc[kSampled];
-        const uint32_t Q =
-            (uint32_t)(((uint64_t)kSpecNum * K * sampled + (uint64_t)kSpecDen * V - 1u) / ((uint64_t)kSpecDen * V)) + 2u;
-        const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, Q, false, lane), T, lane);
+        const uint32_t tkey = K <= kSpecMaxK ? lower_past_ties(hist_select(L.coarse, L.fine, spec_q(), false, lane), T, lane) : 0u;
         // A bounded threshold key is above 0x007fffff (lower_past_ties), so
         // 1 is free to say "not bounded".
         (void)lds_publish(&L.misc[kTauState], tkey ? tkey : 1u);
@@ -673,14 +790,27 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   // wave selects the threshold instead): their ids are fetched while the
   // other waves' rows are still landing, and counted while they wait for
   // the threshold, so the waves whose rows land last find the counts done.
-  if (arrive < kTauWaves - 1u) count_history(arrive, kTauWaves - 1u);
+  if (cmode) {
+    // The first wave to land slides the count table and announces it once
+    // its atomics are complete in L2.
+    if (!cplan.rebuild && arrive == 0u) {
+      counts_slide(a, b, cplan);
+      counts_publish();
+      lds_signal(&L.misc[kSyncHist]);
+    }
+  } else if (arrive < kTauWaves - 1u) {
+    count_history(arrive, kTauWaves - 1u);
+  }
 
   // 3. The scan: every lane whose maximum over a chunk reaches the
   //    published threshold appends one entry (the chunk's 4 values and its
   //    position) to the wave's region: one compare per chunk, and for the
   //    chunks where some lane hits, one ballot offset and two LDS writes.
   const uint32_t tau = lds_wait_nonzero(&L.misc[kTauState], 1u, a);
-  if (tau <= 1u) return false;  // every wave read the same published state
+  // Not bounded by the sample (a large K, or a long run of ties after the
+  // division by T): the proven threshold below takes the row. Every wave
+  // read the same published state.
+  const bool spec = tau > 1u;
   float tf = key2f(tau);
   LLMHIP_MARK(4);
   uint32_t nent = 0u;  // this wave's entries
@@ -696,8 +826,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       nent += (uint32_t)__popcll((unsigned long long)m);
     }
   };
+  if (spec) {
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) scan_chunk(c, mc[c]);
+    for (int c = 0; c < NCH; ++c) scan_chunk(c, mc[c]);
+  }
   LLMHIP_MARK(5);
 
   // 5. Settle this wave's entries: each lane takes an entry and handles its
@@ -706,9 +838,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   //    division, generate.rs:357-359), appended to ord[] with one LDS
   //    atomic per round.
   uint32_t pmv = 0u;
+  uint32_t slot_n = kCandN, slot_o = kOverflow;  // the pass's candidate count and overflow flag
   auto settle = [&]() __attribute__((always_inline)) {
     if (__builtin_expect(nent > kEntries, 0)) {
-      if (lane == 0) atomicOr(&L.misc[kOverflow], 1u);
+      if (lane == 0) atomicOr(&L.misc[slot_o], 1u);
       return;
     }
     for (uint32_t k0 = 0; k0 < nent; k0 += 64u) {
@@ -726,7 +859,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       // The entry's owner is a lane of this wave: fetch its mask words.
       const uint32_t owner = pos_owner<NCH>(base);
       const uint32_t mkown = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((owner & 63u) << 2), (int)mkbits);
-      const uint32_t pmown = (!use_pen || k >= nent) ? 0u : L.pm[owner];
+      const uint32_t pmown = (!use_pen || k >= nent) ? 0u : cmode ? 0xffffffffu : L.pm[owner];
       while (__ballot(rem != 0u)) {
         // A lane takes part in a round only while it has a hit left.
         bool ok = rem != 0u;
@@ -742,14 +875,17 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
         const uint64_t mk = __ballot(ok);
         if (mk) {
           uint32_t o = 0u;
-          if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
+          if (lane == 0) o = atomicAdd(&L.misc[slot_n], (uint32_t)__popcll((unsigned long long)mk));
           o = readlane_u32(o, 0) + lanes_below(mk);
           if (ok && o < kFastCand) L.ord[o] = cand_order(f2key(v / T), pos);
         }
       }
     }
   };
-  if (use_pen) {
+  if (cmode) {
+    lds_wait(&L.misc[kSyncHist], 1u, a);
+    if (use_pen) pmv = 0xffffffffu;
+  } else if (use_pen) {
     lds_wait(&L.misc[kSyncHist], kTauWaves - 1u, a);
     pmv = L.pm[tid];
   }
@@ -757,51 +893,162 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   lds_barrier();
   LLMHIP_MARK(6);
   uint32_t n = L.misc[kCandN];
+  bool ovf = L.misc[kOverflow] != 0u;
   LLMHIP_NOTE(12, n);
-  if (__builtin_expect(n < K || n > kFastCand || L.misc[kOverflow], 0)) {
-    LLMHIP_NOTE(13, 1);
-    // The speculative threshold failed: use the exact one, the lower edge of
-    // the fine bin holding the K-th largest of the 1024 per-thread maxima of
-    // the masked, penalized row (at least K values lie at or above it, in
-    // the threads whose maximum does). Everyone is past the sample
-    // histogram, so it is reused.
-    fix_all(pmv);
-    float tm = -INFINITY;
+  // A speculative threshold the penalty undercut (a history holding the
+  // row's own top ids): once more from the sample histogram, at a position
+  // deeper by the factor the settle fell short of 5K/4 (at most 8). One
+  // wave selects it (a selection in every wave would compete for the ALUs).
+  if (__builtin_expect(spec && n < K && !ovf, 0)) {
+    if (wave == 0u) {
+      const uint64_t q = spec_q();
+      const uint64_t want = n ? (q * 5u * K + 4u * n - 1u) / (4u * n) : 8u * q;
+      const uint64_t q2 = want < 8u * q ? want : 8u * q;
+      const uint32_t tk2 = lower_past_ties(hist_select(L.coarse, L.fine, (uint32_t)q2, false, lane), T, lane);
+      (void)lds_publish(&L.misc[kTau2], tk2 != 0u && key2f(tk2) < tf ? tk2 : 1u);
+    }
+    const uint32_t tk2 = lds_wait_nonzero(&L.misc[kTau2], 1u, a);
+    const bool again = tk2 > 1u;
+    if (again) {
+      LLMHIP_NOTE(13, 4u);
+      LLMHIP_MARK(11);
+      tf = key2f(tk2);
+      nent = 0u;
+      slot_n = kCandN2;
+      slot_o = kOverflow2;
 #pragma unroll
-    for (int e = 0; e < NCH * 4; ++e) tm = fmaxf(tm, x[e]);
+      for (int c = 0; c < NCH; ++c) scan_chunk(c, mc[c]);
+      LLMHIP_MARK(12);
+      settle();
+      LLMHIP_MARK(13);
+    }
+    lds_barrier();  // the pass is settled, and every wave is past the histogram reads
+    if (again) {
+      n = L.misc[kCandN2];
+      ovf = L.misc[kOverflow2] != 0u;
+      LLMHIP_NOTE(15, n);
+    }
+  }
+  if (__builtin_expect(!spec || n < K || n > kFastCand || ovf, 0)) {
+    LLMHIP_NOTE(13, spec ? 1u : 2u);
+    // The proven threshold. Known values are those of the slots outside the
+    // history and the mask: final without a penalty, which (rp >= 1) only
+    // lowers a value. t0 is the lower edge of the fine bin holding the K-th
+    // largest of the 1024 per-thread known maxima, so at least K known
+    // values lie at or above it, and a history slot can reach it only if
+    // its raw value does. The scan and settle run again at t0 (lowered past
+    // ties after the division by T): at least K candidates. Everyone is past
+    // the sample histogram and the scan entries, so their LDS is reused.
+    const uint32_t pmr = cmode && use_pen ? table_bits() : pmv;
+    const uint32_t known = ~(pmr | mkbits);
+    const float tm = known_max(pmr);
     reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
     lds_barrier();  // every wave has read the candidate count and overflow flag above
+    LLMHIP_MARK(11);
     if (tid == 0) {
       L.misc[kCandN] = 0u;
       L.misc[kOverflow] = 0u;
     }
+    slot_n = kCandN;
+    slot_o = kOverflow;
     if (tm > -INFINITY) {
       const uint32_t k = f2key(tm);
       atomicAdd(&L.coarse[k >> 24], 1u);
       atomicAdd(&L.fine[k >> 20], 1u);
     }
-    lds_barrier();  // the histogram and the reset words, before the appends
-    const uint32_t tkey = lower_past_ties(hist_select(L.coarse, L.fine, K, true, lane), T, lane);
-    if (tkey == 0u) return false;
-    tf = key2f(tkey);
-    // Values are final now (fixed in place): every lane appends its own
-    // values at or above the threshold, one ballot per slot, with no scan
-    // entries (so no per-wave region can overflow).
-#pragma unroll
-    for (int e = 0; e < NCH * 4; ++e) {
-      const bool ok = x[e] >= tf;
-      const uint64_t mk = __ballot(ok);
-      if (mk) {
-        uint32_t o = 0u;
-        if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
-        o = readlane_u32(o, 0) + lanes_below(mk);
-        if (ok && o < kFastCand)
-          L.ord[o] = cand_order(f2key(x[e] / T), chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3));
-      }
-    }
     lds_barrier();
+    // A finite maximum's key is at least 0x00800000, above -inf's and NaN's
+    // (hist_locate's 0 says fewer than K threads hold a known value).
+    if (wave == 0u) {
+      const uint32_t t0 = hist_locate(L.coarse, L.fine, K, lane).lo;
+      const uint32_t tk = t0 ? lower_past_ties(t0, T, lane) : 0u;
+      (void)lds_publish(&L.misc[kTau0], tk ? tk : 1u);
+    }
+    const uint32_t tk0 = lds_wait_nonzero(&L.misc[kTau0], 1u, a);
+    if (tk0 <= 1u) return false;
+    LLMHIP_MARK(12);
+    tf = key2f(tk0);
+    nent = 0u;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) scan_chunk(c, mc[c]);
+    settle();
+    lds_barrier();
+    LLMHIP_MARK(13);
     n = L.misc[kCandN];
+    if (__builtin_expect(n > kFastCand || L.misc[kOverflow], 0)) {
+      // Too many values at or above the threshold for the scan entries or
+      // the list (a large K): narrow it per slot. Level 1: the fine bin
+      // holding the K-th largest known value at or above it (tk0 <= t0, so
+      // at least K are). Level 2, when that bin is
+      // crowded: 12 more key bits inside it. At least K final values lie at
+      // or above the result.
+      LLMHIP_NOTE(13, 3u);
+      uint32_t* fine1 = reinterpret_cast<uint32_t*>(L.ent);  // kWaves * kEntries float4 >= kFineBins words
+      uint32_t* coarse1 = L.etag;                              // kWaves * kEntries words >= kCoarseBins
+      reinterpret_cast<uint4*>(fine1)[tid] = make_uint4(0u, 0u, 0u, 0u);
+      if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(coarse1)[tid] = make_uint4(0u, 0u, 0u, 0u);
+      lds_barrier();  // every wave has read the count and flag, and is past the entries
+      if (tid == 0) {
+        L.misc[kCandN] = 0u;
+        L.misc[kOverflow] = 0u;
+      }
+#pragma unroll
+      for (int e = 0; e < NCH * 4; ++e) {
+        const uint32_t k = f2key(x[e]);
+        if (((known >> e) & 1u) && k >= tk0) {
+          atomicAdd(&coarse1[k >> 24], 1u);
+          atomicAdd(&fine1[k >> 20], 1u);
+        }
+      }
+      lds_barrier();  // level 1 counted; every wave is past level 0's reads
+      const HistPos h1 = hist_locate(coarse1, fine1, K, lane);
+      LLMHIP_NOTE(14, h1.cnt);
+      uint32_t thr = h1.lo;
+      if (h1.cnt > kRefineCount) {
+        reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
+        if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
+        lds_barrier();
+#pragma unroll
+        for (int e = 0; e < NCH * 4; ++e) {
+          const uint32_t k = f2key(x[e]);
+          if (((known >> e) & 1u) && (k >> 20) == (h1.lo >> 20)) {
+            const uint32_t k2 = k << 12;
+            atomicAdd(&L.coarse[k2 >> 24], 1u);
+            atomicAdd(&L.fine[k2 >> 20], 1u);
+          }
+        }
+        lds_barrier();
+        thr = h1.lo | (hist_locate(L.coarse, L.fine, h1.need, lane).lo >> 12);
+      }
+      const uint32_t tkey = lower_past_ties(thr, T, lane);
+      if (tkey == 0u) return false;
+      LLMHIP_MARK(14);
+      tf = key2f(tkey);
+      // Every lane appends its own final values at or above the threshold,
+      // one ballot per slot, with no scan entries (so no per-wave region can
+      // overflow).
+#pragma unroll
+      for (int e = 0; e < NCH * 4; ++e) {
+        const uint32_t pos = chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3);
+        float v = x[e];
+        bool ok = v >= tf && ((mkbits >> e) & 1u) == 0u;
+        if (ok && ((pmr >> e) & 1u)) {
+          v = apply_penalty(v, count_of(pos), rp);
+          ok = v >= tf;
+        }
+        const uint64_t mk = __ballot(ok);
+        if (mk) {
+          uint32_t o = 0u;
+          if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
+          o = readlane_u32(o, 0) + lanes_below(mk);
+          if (ok && o < kFastCand) L.ord[o] = cand_order(f2key(v / T), pos);
+        }
+      }
+      lds_barrier();
+      LLMHIP_MARK(15);
+      n = L.misc[kCandN];
+    }
     // Heavy ties or an unusually flat top: not bounded by the register path.
     if (n < K || n > kFastCand) return false;
   }

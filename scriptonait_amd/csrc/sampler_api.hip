@@ -25,6 +25,7 @@ static __device__ __align__(256) uint32_t scratch[LLMHIP_NOALLOC_SCRATCH_BYTES /
 
 namespace llmhip {
 hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s);
+hipError_t launch_fast_counts(const SampleArgs& a, bool vec, hipStream_t s);
 hipError_t launch_general(const SampleArgs& a, hipStream_t s);
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
@@ -204,6 +205,9 @@ struct RingArgs {
   const uint32_t* hist_start = nullptr;
   uint32_t cap = 0;
   uint32_t window = 0;
+  uint32_t* counts = nullptr;   // count table (nullable)
+  uint32_t* counted = nullptr;
+  uint64_t counts_words = 0;
 };
 
 int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
@@ -258,6 +262,9 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.hist_start = ring.hist_start;
   a.ring_cap = ring.cap;
   a.window = ring.window;
+  a.counts = ring.counts;
+  a.counted = ring.counted;
+  a.counts_words = ring.counts_words;
   a.allowed = mask.len ? mask.bytes : nullptr;
   a.allowed_bits = mask.len && !mask.bytes ? mask.bits : nullptr;
   a.allowed_len = (uint32_t)mask.len;
@@ -288,7 +295,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
       a.slotmask = sm;
     }
     a.row_class_mask = fast_mask;
-    HIP_TRY(launch_fast(a, vec, s));
+    HIP_TRY(a.counts ? launch_fast_counts(a, vec, s) : launch_fast(a, vec, s));
   }
   if (vocab_mask) {
     a.row_class_mask = vocab_mask;
@@ -321,7 +328,8 @@ namespace {
 int decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
                 const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
                 uint32_t* ring_len, uint32_t* done, const uint32_t* hist_start, size_t window, const Mask& mask,
-                const void* mask_ptr, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids, void* stream) {
+                const void* mask_ptr, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids, void* stream,
+                uint32_t* counts = nullptr, size_t counts_words = 0, uint32_t* counted = nullptr) {
   if (!ctx) return arg_fail("ctx is null");
   int st = validate(B, V, ld, logits, params, nullptr, nullptr, mask_ptr, mask.len, rng_state, out_ids);
   if (st || B == 0) return st;
@@ -330,6 +338,11 @@ int decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t
   if (!ring || !ring_len) return arg_fail("ring and ring_len are required");
   if (ring_cap == 0 || ring_cap > 0x7fffffffu) return arg_fail("ring_cap must be in 1 .. 2^31-1");
   if (window > ring_cap) return arg_fail("window must not exceed ring_cap");
+  if (counts || counted) {
+    if (!counts || !counted) return arg_fail("counts and counted go together");
+    if (counts_words < (V + 1) / 2) return arg_fail("counts_words must be at least (V + 1) / 2");
+    if (window >= 65536) return arg_fail("a count table holds windows below 65536 tokens");
+  }
   Device d(ctx->device);
   if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -343,6 +356,9 @@ int decode_step(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t
   r.hist_start = hist_start;
   r.cap = (uint32_t)ring_cap;
   r.window = (uint32_t)window;
+  r.counts = counts;
+  r.counted = counted;
+  r.counts_words = counts_words;
   return enqueue(ctx, logits, B, V, ld, params, params_stride, pdev, nullptr, nullptr, mask, eos_id, rng_state,
                  out_ids, nullptr, nullptr, s, false, r);
 }
@@ -671,6 +687,20 @@ int llmhip_decode_step_bits(llmhip_ctx* ctx, const float* logits, size_t B, size
   m.len = allowed_len;
   return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, hist_start,
                      window, m, allowed_bits, eos_id, rng_state, out_ids, stream);
+}
+
+int llmhip_decode_step_counts(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
+                              const llmhip_params* params, size_t params_stride, uint32_t* ring, size_t ring_cap,
+                              uint32_t* ring_len, uint32_t* done, const uint32_t* hist_start, size_t window,
+                              uint32_t* counts, size_t counts_words, uint32_t* counted, const uint8_t* allowed,
+                              size_t allowed_len, uint32_t eos_id, uint64_t* rng_state, uint32_t* out_ids,
+                              void* stream) {
+  if (!counts || !counted) return arg_fail("counts and counted are required");
+  Mask m;
+  m.bytes = allowed;
+  m.len = allowed_len;
+  return decode_step(ctx, logits, B, V, ld, params, params_stride, ring, ring_cap, ring_len, done, hist_start,
+                     window, m, allowed, eos_id, rng_state, out_ids, stream, counts, counts_words, counted);
 }
 
 int llmhip_ctx_status(llmhip_ctx* ctx, void* stream, llmhip_status* out) {

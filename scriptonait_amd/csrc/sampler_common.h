@@ -77,6 +77,15 @@ struct SampleArgs {
   const uint32_t* hist_start;
   uint32_t ring_cap;
   uint32_t window;
+  // Decode-step mode, nullable: a count table per generation. counts[b *
+  // counts_words + (id >> 1)] holds the u16 multiplicity of id in half
+  // (id & 1), over the ring tokens counted[2b] .. counted[2b + 1] (counted
+  // since the generation's start, as ring_len counts). Each step moves that
+  // range to the row's window and the kernels read the multiplicities from
+  // the table instead of walking the window (see counts_plan below).
+  uint32_t* counts;
+  uint32_t* counted;
+  uint64_t counts_words;
   // Device word of kStatus* bits, set by a kernel that hit an internal
   // limit (zero after a correct call).
   uint32_t* status;
@@ -147,6 +156,119 @@ __device__ __forceinline__ void store_result(const SampleArgs& a, uint32_t b, ui
       a.ring[(size_t)b * a.ring_cap + len_b % a.ring_cap] = id;
       a.ring_len[b] = len_b + 1u;
     }
+  }
+}
+
+// The count table (decode-step mode with counts): at the start of a step
+// the table holds the ring tokens [cs, ce); the window is [ts, te) = [len -
+// H, len). When the window only slid (cs <= ts <= ce <= te), by at most
+// kCountsDelta tokens in all, the tokens leaving are still in the ring and
+// the table held something (an empty range leaves its contents unknown),
+// one wave applies the change: -1 for tokens [cs, ts), +1 for [ce, te), as
+// device-scope integer atomics (their order does not matter). Otherwise
+// (the first step, a cache reset, a skipped step) the whole workgroup
+// rebuilds the row: zero, then +1 per window token. Ids >= V are not
+// counted, as the penalty ignores them (generate.rs:343-352).
+constexpr uint32_t kCountsDelta = 32;
+
+struct CountsPlan {
+  uint32_t cs, ce, ts, te;
+  bool rebuild;
+};
+
+// cs, ce: counted[2b], counted[2b + 1] as the row read them.
+__device__ __forceinline__ CountsPlan counts_plan(const SampleArgs& a, uint32_t cs, uint32_t ce, uint32_t len,
+                                                  uint32_t H) {
+  CountsPlan p;
+  p.cs = cs;
+  p.ce = ce;
+  p.te = len;
+  p.ts = len - H;
+  // An empty range says nothing about the table's contents (a generation's
+  // first step): rebuild.
+  p.rebuild = !(p.cs < p.ce && p.cs <= p.ts && p.ts <= p.ce && p.ce <= p.te &&
+                (p.ts - p.cs) + (p.te - p.ce) <= kCountsDelta && p.te - p.cs <= a.ring_cap);
+  return p;
+}
+
+__device__ __forceinline__ uint32_t* counts_row(const SampleArgs& a, uint32_t b) {
+  return a.counts + (size_t)b * a.counts_words;
+}
+
+__device__ __forceinline__ uint32_t ring_token(const SampleArgs& a, uint32_t b, uint32_t t) {
+  return a.ring[(size_t)b * a.ring_cap + t % a.ring_cap];
+}
+
+// Waits until this wave's table stores and atomics have been performed in
+// L2, where the atomics execute and where counts_at's device-scope loads
+// read. That is all the waves of one workgroup need (they share the L2 of
+// their XCD); a device-scope release fence would also write back the
+// XCD's whole L2 (buffer_wbl2) once per row and step. The next launch sees
+// the table through the kernel boundary's own cache maintenance.
+__device__ __forceinline__ void counts_publish() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// The small change, by one wave (all 64 lanes). The new range is stored.
+__device__ __forceinline__ void counts_slide(const SampleArgs& a, uint32_t b, const CountsPlan& p) {
+  const uint32_t lane = threadIdx.x & 63u;
+  uint32_t* row = counts_row(a, b);
+  const uint32_t nout = p.ts - p.cs, nin = p.te - p.ce;  // nout + nin <= kCountsDelta <= 64
+  if (lane < nout) {
+    const uint32_t id = ring_token(a, b, p.cs + lane);
+    if (id < a.V) atomicSub(&row[id >> 1], 1u << ((id & 1u) << 4));
+  } else if (lane < nout + nin) {
+    const uint32_t id = ring_token(a, b, p.ce + lane - nout);
+    if (id < a.V) atomicAdd(&row[id >> 1], 1u << ((id & 1u) << 4));
+  }
+  if (lane == 0) {
+    a.counted[2 * (size_t)b] = p.ts;
+    a.counted[2 * (size_t)b + 1] = p.te;
+  }
+}
+
+// The rebuild, by the whole workgroup (every thread calls it); ends with a
+// workgroup barrier after which the row is complete in L2. A workgroup
+// barrier alone does not wait for other waves' global writes to reach L2,
+// where the atomics execute: every thread publishes its writes before each
+// barrier.
+__device__ __forceinline__ void counts_rebuild(const SampleArgs& a, uint32_t b, const CountsPlan& p) {
+  uint32_t* row = counts_row(a, b);
+  const uint32_t words = (a.V + 1u) / 2u;
+  for (uint32_t i = threadIdx.x; i < words; i += blockDim.x)
+    __hip_atomic_store(&row[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  counts_publish();
+  __syncthreads();
+  for (uint32_t j = threadIdx.x; j < p.te - p.ts; j += blockDim.x) {
+    const uint32_t id = ring_token(a, b, p.ts + j);
+    if (id < a.V) atomicAdd(&row[id >> 1], 1u << ((id & 1u) << 4));
+  }
+  if (threadIdx.x == 0) {
+    a.counted[2 * (size_t)b] = p.ts;
+    a.counted[2 * (size_t)b + 1] = p.te;
+  }
+  counts_publish();
+  __syncthreads();
+}
+
+// Id's multiplicity in the row's table (after the step's change is
+// published: device-scope loads, past the CU's cache, read L2).
+__device__ __forceinline__ uint32_t counts_at(const SampleArgs& a, uint32_t b, uint32_t id) {
+  const uint32_t w = __hip_atomic_load(&counts_row(a, b)[id >> 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (w >> ((id & 1u) << 4)) & 0xffffu;
+}
+
+// The step's table change for the sorting and full-vocabulary paths (every
+// thread calls it): those count the window themselves, so the table is only
+// kept current for the next step. Ends with every change complete.
+__device__ __forceinline__ void counts_advance_all(const SampleArgs& a, uint32_t b, uint32_t len, uint32_t H) {
+  const CountsPlan p = counts_plan(a, a.counted[2 * (size_t)b], a.counted[2 * (size_t)b + 1], len, H);
+  if (p.rebuild) {
+    counts_rebuild(a, b, p);
+  } else {
+    if (threadIdx.x < 64u) {
+      counts_slide(a, b, p);
+      counts_publish();
+    }
+    __syncthreads();
   }
 }
 

@@ -1156,6 +1156,9 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   }
   const uint32_t len_b = h0;
   const HistRow hr = hist_row(a, b, h0, h1);
+  // The count table is kept current for the next step; this path counts the
+  // window itself.
+  if (a.ring_cap && a.counts) counts_advance_all(a, b, len_b, hr.H);
   const float rp = P.repetition_penalty, T = P.temperature;
   const bool use_pen = rp != 1.0f && hr.H > 0;
   __syncthreads();

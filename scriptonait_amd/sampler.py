@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "llmhip_sample_device_noalloc",
     "llmhip_sample_tied_head_device",
     "llmhip_decode_step",
+    "llmhip_decode_step_counts",
     "llmhip_seen_tokens",
     "llmhip_sample_device_bits",
     "llmhip_decode_step_bits",
@@ -113,6 +114,9 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.llmhip_decode_step.restype = ctypes.c_int
     decode = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, sz, vp, sz, u32, vp, vp, vp]
     lib.llmhip_decode_step.argtypes = decode
+    lib.llmhip_decode_step_counts.restype = ctypes.c_int
+    lib.llmhip_decode_step_counts.argtypes = [vp, vp, sz, sz, sz, vp, sz, vp, sz, vp, vp, vp, sz, vp, sz, vp, vp, sz,
+                                              u32, vp, vp, vp]
     lib.llmhip_sample_device_bits.restype = ctypes.c_int
     lib.llmhip_sample_device_bits.argtypes = common + [vp]
     lib.llmhip_decode_step_bits.restype = ctypes.c_int
@@ -340,14 +344,16 @@ class Sampler:
 
     def decode_step(self, logits, params: np.ndarray, ring, ring_len, done, window: int, rng_state, out_ids,
                     V: Optional[int] = None, allowed=None, eos_id: int = EOS, stream=None, allowed_bits=None,
-                    allowed_len: Optional[int] = None, hist_start=None) -> None:
+                    allowed_len: Optional[int] = None, hist_start=None, counts=None, counted=None) -> None:
         """llmhip_decode_step on torch CUDA tensors: one Generator::step
         (generate.rs:157-165) for B generations whose history ring
         ([B, ring_cap] int32), lengths and done flags ([B] int32) and RNG
         states ([B] int64 viewed as u64) live on the device; hist_start
         ([B] int32, optional) is the first ring token still in each row's
-        model cache. Enqueued on `stream` (default: torch's current stream);
-        does not synchronize."""
+        model cache. With counts ([B, >= (V+1)//2] int32, the u16 count
+        table) and counted ([B, 2] int32) it calls llmhip_decode_step_counts
+        (incremental history counts). Enqueued on `stream` (default: torch's
+        current stream); does not synchronize."""
         import torch
 
         B, ld = logits.shape
@@ -357,7 +363,14 @@ class Sampler:
         if stream is None:
             stream = torch.cuda.current_stream(logits.device)
         dp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-        if allowed_bits is not None:
+        if counts is not None:
+            if allowed_bits is not None:
+                raise ValueError("counts go with the byte mask (allowed), not allowed_bits")
+            status = self.lib.llmhip_decode_step_counts(
+                self.ctx, dp(logits), B, V, ld, _ptr(params), stride, dp(ring), ring.shape[1], dp(ring_len),
+                dp(done), dp(hist_start), window, dp(counts), counts.shape[1], dp(counted), dp(allowed),
+                0 if allowed is None else allowed.numel(), eos_id, dp(rng_state), dp(out_ids), stream.cuda_stream)
+        elif allowed_bits is not None:
             if allowed is not None:
                 raise ValueError("pass allowed or allowed_bits, not both")
             status = self.lib.llmhip_decode_step_bits(

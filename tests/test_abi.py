@@ -44,7 +44,7 @@ def test_params_struct_layout_matches_header():
 
 def test_version_and_status_strings():
     lib = smp.load_library()
-    assert lib.llmhip_abi_version() == 6
+    assert lib.llmhip_abi_version() == 7
     assert lib.llmhip_status_string(0) == b"ok"
     assert lib.llmhip_status_string(-1) == b"invalid argument"
     assert lib.llmhip_status_string(-2) == b"no HIP device"

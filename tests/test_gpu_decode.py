@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_len=None, max_prompt=300,
-         eos_rows=1):
+         eos_rows=1, counts=False):
     import torch
 
     from oracle import oracle
@@ -46,6 +46,10 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_l
     hist = [list(p) for p in prompts]
     cache = [list(p) for p in prompts]  # the model cache's tokens (recent_tokens reads these)
     d_start = torch.zeros(B, dtype=torch.int32, device=dev) if context_len else None
+    d_counts = d_counted = None
+    if counts:  # the table starts as garbage: a zero counted range makes the first step rebuild it
+        d_counts = torch.from_numpy(rs.integers(0, 2**31, size=(B, (V + 1) // 2)).astype(np.int32)).to(dev)
+        d_counted = torch.zeros((B, 2), dtype=torch.int32, device=dev)
     resets = 0
     done = np.zeros(B, dtype=bool)
     st = rng0.copy()
@@ -55,7 +59,7 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_l
             if (b + 3 * t) % 29 == 0:
                 logits[b, EOS_ID] = 60.0
         sampler.decode_step(torch.from_numpy(logits).to(dev), prm, d_ring, d_len, d_done, window, d_rng, d_ids,
-                            hist_start=d_start)
+                            hist_start=d_start, counts=d_counts, counted=d_counted)
         live = np.nonzero(~done)[0]
         want = np.full(B, EOS_ID, dtype=np.uint32)
         if live.size:
@@ -89,6 +93,23 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_l
         n = len(hist[b])
         for j in range(max(0, n - cap), n):
             assert gring[b, j % cap] == hist[b][j], (b, j)
+    if counts:
+        # The table holds the window that the last step of each row used:
+        # counted = [len - H, len) at that step; its multiplicities are the
+        # window's (ids >= V are not counted).
+        tab = d_counts.cpu().numpy().view(np.uint32)
+        cnt = d_counted.cpu().numpy().view(np.uint32)
+        for b in range(B):
+            lo, hi = int(cnt[b, 0]), int(cnt[b, 1])
+            assert 0 <= lo <= hi <= len(hist[b])
+            want = np.zeros(V, dtype=np.int64)
+            for tok in hist[b][lo:hi]:
+                if tok < V:
+                    want[tok] += 1
+            got = np.stack([tab[b] & 0xFFFF, tab[b] >> 16], axis=1).reshape(-1)[:V]
+            assert np.array_equal(got, want), b
+        return resets
+    return resets
 
 
 def test_decode_loop_top_k_path(sampler):
@@ -130,3 +151,30 @@ def test_decode_step_rejects_an_empty_vocabulary(sampler):
 
 def test_decode_loop_greedy(sampler):
     _run(sampler, 8192, make_params(0.0, 64, 0.95, 0.05, 1.3))
+
+
+@pytest.mark.parametrize("path", ["top_k", "full_vocab", "greedy"])
+def test_decode_loop_with_count_table(sampler, path):
+    """llmhip_decode_step_counts: the same ids, rings and RNG states as the
+    CPU loop, and a count table equal to the window's multiplicities."""
+    if path == "top_k":
+        _run(sampler, 32000, make_params(0.7, 64, 0.95, 0.05, 1.15), counts=True)
+    elif path == "full_vocab":
+        _run(sampler, 2048, make_params(1.0, 0, 0.9, 0.02, 1.8), window=16, cap=17, counts=True)
+    else:
+        _run(sampler, 8192, make_params(0.0, 64, 0.95, 0.05, 1.3), counts=True)
+
+
+def test_decode_loop_with_count_table_and_cache_resets(sampler):
+    """hist_start jumps at each cache reset: the table is rebuilt there and
+    slid between resets."""
+    resets = _run(sampler, 32000, make_params(0.7, 64, 0.95, 0.05, 1.15), steps=40, window=48, cap=64,
+                  context_len=64, max_prompt=60, eos_rows=2, counts=True)
+    assert resets > 0
+
+
+def test_decode_loop_with_a_long_window_count_table(sampler):
+    """A 3000-token window (prompts of up to 4000 uniform tokens, so ids repeat):
+    the table slides one token a step over a long window."""
+    _run(sampler, 32000, make_params(0.7, 64, 0.95, 0.05, 1.15), steps=12, B=8, window=3000, cap=4096,
+         max_prompt=4000, counts=True)

@@ -6,6 +6,7 @@ path) at reduced batch.
 import numpy as np
 import pytest
 
+from oracle import oracle
 from parity_util import compare, run_both
 from scriptonait_amd.workloads import PARAMS_DTYPE, make_params, make_workload
 
@@ -179,3 +180,35 @@ def test_exact_ties_in_the_top_p_and_draw_folds(sampler, V):
     assert np.array_equal(g.ids, o.ids), np.nonzero(g.ids != o.ids)[0]
     assert np.array_equal(g.kept, o.kept)
     assert np.array_equal(g.rng_state, o.rng_state)
+
+
+@pytest.mark.parametrize("V,temp,k", [(32000, 0.7, 64), (32000, 0.0, 64), (12345, 1.0, 40), (4099, 0.0, 8),
+                                      (32000, 1.0, 700)])
+def test_history_of_each_rows_top_candidates(sampler, V, temp, k):
+    """The history holds each row's own highest logits, 1-4 times each, plus
+    random ids (a long generation's window: what was drawn is what ranks
+    high). The penalty pushes most of the raw top below the speculative
+    threshold, so the register path must take its proven threshold, and
+    greedy rows their bounded penalty pass; every row must still match the
+    oracle and none may be handed to the sorting path."""
+    B = 24
+    w = make_workload(3, B=B, V=V)
+    rs = np.random.default_rng(V + k)
+    rows = []
+    for b in range(B):
+        top = np.argsort(-w.logits[b, :V], kind="stable")[: 3 * k]
+        reps = rs.integers(1, 5, size=top.size)
+        ids = np.concatenate([np.repeat(top, reps), rs.integers(0, V, size=2000)]).astype(np.uint32)
+        rows.append(rs.permutation(ids))
+    offs = np.concatenate([[0], np.cumsum([r.size for r in rows])]).astype(np.uint32)
+    hist = np.concatenate(rows)
+    prm = make_params(temp, k, 0.95, 0.02, 1.3)
+    sampler.status()  # clears the hand-over count
+    g = sampler.sample_host(w.logits, prm, w.rng_seeds, hist, offs, V=V, want_probs=temp > 0)
+    handovers = sampler.status().handovers
+    o = oracle.sample_batch(w.logits, prm, w.rng_seeds, hist, offs, V=V, want_probs=temp > 0, threads=8)
+    if temp > 0:
+        compare(g, o, f"top-candidate history V={V} k={k}")
+    else:
+        assert np.array_equal(g.ids, o.ids)
+    assert handovers == 0
