@@ -5,8 +5,8 @@
 
 namespace llmhip {
 
-hipError_t launch_fast_counts(const SampleArgs& a, bool vec, hipStream_t s) {
-  return launch_fast_mode<true>(a, vec, s);
+hipError_t launch_fast_counts(const SampleArgs& a, bool vec, bool bigk, hipStream_t s) {
+  return launch_fast_mode<true>(a, vec, bigk, s);
 }
 
 }  // namespace llmhip

@@ -8,49 +8,56 @@
 
 namespace llmhip {
 
-template <int NCH, bool VEC, bool GREEDY, bool CMODE>
+static_assert(kMaxFastK <= kSelCap, "hand-overs select in LDS");
+
+template <int NCH, bool VEC, bool GREEDY, bool CMODE, bool BIGK>
 __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
-  __shared__ FastLds<NCH> L;
-  if (__builtin_expect(!fast_row<NCH, VEC, GREEDY, CMODE>(a, L), 0)) {
+  __shared__ FastLds<NCH, BIGK> L;
+  if (__builtin_expect(!fast_row<NCH, VEC, GREEDY, CMODE, BIGK>(a, L), 0)) {
     if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
     __syncthreads();
-    general_row(a, blockIdx.x, L.gen, true);
+    general_row<false>(a, blockIdx.x, L.gen, true);  // greedy or K <= 1024: no whole-row sort
   }
 }
 
 // One launch per row class present: greedy rows and top-k rows run in
-// kernels compiled apart, so neither carries the other's registers.
+// kernels compiled apart, so neither carries the other's registers. bigk:
+// some top-k row has K > 64.
 template <int NCH, bool CMODE>
-hipError_t launch_fast_nch(const SampleArgs& a0, bool vec, hipStream_t s) {
+hipError_t launch_fast_nch(const SampleArgs& a0, bool vec, bool bigk, hipStream_t s) {
   SampleArgs a = a0;
   if (a0.row_class_mask & kClassGreedy) {
     a.row_class_mask = kClassGreedy;
     if (vec) {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, true, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, true, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
     } else {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, true, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, true, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (a0.row_class_mask & kClassTopK) {
     a.row_class_mask = kClassTopK;
-    if (vec) {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+    if (vec && bigk) {
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE, true>), dim3(a.B), dim3(kBlock), 0, s, a);
+    } else if (vec) {
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
+    } else if (bigk) {
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE, true>), dim3(a.B), dim3(kBlock), 0, s, a);
     } else {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
     }
   }
   return hipGetLastError();
 }
 
 template <bool CMODE>
-hipError_t launch_fast_mode(const SampleArgs& a, bool vec, hipStream_t s) {
+hipError_t launch_fast_mode(const SampleArgs& a, bool vec, bool bigk, hipStream_t s) {
   switch (fast_nch(a.V)) {
-    case 1: return launch_fast_nch<1, CMODE>(a, vec, s);
-    case 2: return launch_fast_nch<2, CMODE>(a, vec, s);
-    case 4: return launch_fast_nch<4, CMODE>(a, vec, s);
-    default: return launch_fast_nch<8, CMODE>(a, vec, s);
+    case 1: return launch_fast_nch<1, CMODE>(a, vec, bigk, s);
+    case 2: return launch_fast_nch<2, CMODE>(a, vec, bigk, s);
+    case 4: return launch_fast_nch<4, CMODE>(a, vec, bigk, s);
+    default: return launch_fast_nch<8, CMODE>(a, vec, bigk, s);
   }
 }
 

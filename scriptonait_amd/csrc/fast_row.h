@@ -90,8 +90,11 @@ constexpr int kOverflow2 = 11; // some wave's region overflowed in it
 constexpr int kTau2 = 12;      // its threshold key (1: no second pass)
 constexpr int kTau0 = 13;      // the proven threshold key (1: not bounded here)
 
-template <int NCH>
+// BIGK: the large-K kernel's scan entries hold 128 per wave (a proven
+// threshold for K up to 1024 puts about 1.2 K chunks in them).
+template <int NCH, bool BIGK = false>
 struct FastLds {
+  static constexpr uint32_t kEnt = BIGK ? 128u : kEntries;
   union {
     uint32_t cnt[NCH * 2048];  // u16 history multiplicities, two per word (V <= NCH*4096)
     GenLds gen;                // the general path's LDS when a row falls back
@@ -99,8 +102,8 @@ struct FastLds {
   uint32_t pm[kBlock];  // per-thread mask: slot is penalized
   __attribute__((aligned(16))) uint32_t coarse[kCoarseBins];
   __attribute__((aligned(16))) uint32_t fine[kFineBins];
-  float4 ent[kWaves * kEntries];     // scan entries: a lane's 4 values of a chunk with a hit
-  __attribute__((aligned(16))) uint32_t etag[kWaves * kEntries];  // chunk position | chunk << 28
+  float4 ent[kWaves * kEnt];  // scan entries: a lane's 4 values of a chunk with a hit
+  __attribute__((aligned(16))) uint32_t etag[kWaves * kEnt];  // chunk position | chunk << 28
   __attribute__((aligned(16))) uint64_t ord[kFastCand];  // settled order keys; then the tail's terms
   uint32_t skey[kMaxFastK];  // sorted top-K: post-temperature key
   uint32_t sid[kMaxFastK];   //               id
@@ -418,11 +421,69 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t* v, uint32_t n) {
   }
 }
 
-// More candidates than the register ranks hold (n <= kFastCand): sort them.
-__device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint32_t n, uint32_t K, uint32_t* skey, uint32_t* sid) {
-  bitonic_sort_desc(ord, n);
-  for (uint32_t i = threadIdx.x; i < K; i += kBlock) {
-    const uint64_t o = ord[i];
+// First index j in [lo, hi) of a descending run with v[j] < x (strict) or
+// v[j] <= x: the number of the run's keys above x (or at or above it) is
+// j - lo. About log2(hi - lo) + 1 LDS reads.
+__device__ __forceinline__ uint32_t desc_bound(const uint64_t* v, uint32_t lo, uint32_t hi, uint64_t x, bool strict) {
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    const uint64_t m = v[mid];
+    if (strict ? m >= x : m > x) {
+      lo = mid + 1u;
+    } else {
+      hi = mid;
+    }
+  }
+  return lo;
+}
+
+// More candidates than the register ranks hold (n <= kFastCand): sort them,
+// descending. Runs of 64 keys are sorted in registers, one key per lane, by
+// a bitonic network of lane exchanges (no barrier); then runs are merged in
+// pairs, log2(n / 64) rounds between v and tmp with one barrier each: a key's
+// place in the merged run is its index in its own run plus its rank in the
+// other run, found by binary search (keys of the first run go before equal
+// keys of the second, which only the zero padding has). The K best are
+// written to skey/sid in sorted order.
+__device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint64_t* tmp, uint32_t n, uint32_t K, uint32_t* skey,
+                                            uint32_t* sid) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t np = (n + 63u) & ~63u;
+  for (uint32_t r = wave; r * 64u < np; r += kWaves) {
+    const uint32_t i = r * 64u + lane;
+    uint64_t x = i < n ? ord[i] : 0ull;
+    for (uint32_t k = 2u; k <= 64u; k <<= 1) {
+      for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
+        const uint64_t y = __shfl_xor(x, (int)j, 64);
+        const bool keep_max = ((lane & k) == 0u) == ((lane & j) == 0u);
+        x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+      }
+    }
+    ord[i] = x;
+  }
+  lds_barrier();
+  uint64_t* src = ord;
+  uint64_t* dst = tmp;
+  for (uint32_t R = 64u; R < np; R <<= 1) {
+    for (uint32_t i = tid; i < np; i += kBlock) {
+      const uint32_t s0 = i & ~(2u * R - 1u);
+      const uint32_t a1 = min(s0 + R, np), b1 = min(s0 + 2u * R, np);
+      const uint64_t x = src[i];
+      uint32_t at;
+      if (i < a1) {  // first run: the second run's keys above x come first
+        at = i + (desc_bound(src, a1, b1, x, false) - a1);
+      } else {       // second run: the first run's keys at or above x come first
+        at = (i - a1) + desc_bound(src, s0, a1, x, true);
+      }
+      dst[at] = x;
+    }
+    lds_barrier();
+    uint64_t* t = src;
+    src = dst;
+    dst = t;
+  }
+  for (uint32_t i = tid; i < K; i += kBlock) {
+    const uint64_t o = src[i];
     skey[i] = (uint32_t)(o >> 32);
     sid[i] = 0xffffffffu - (uint32_t)o;
   }
@@ -435,8 +496,13 @@ __device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint32_t n, uint32_t 
 // the top-k rows only; each variant is compiled without the other's code.
 // CMODE: a decode step with a count table (a.ring and a.counts set); the
 // other calls run variants compiled without the table's code.
-template <int NCH, bool VEC, bool GREEDY, bool CMODE>
-__device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
+// BIGK: some top-k row of the call has K > 64. Without it the kernel holds
+// only the small-K rank and tail (a smaller kernel), and a row with more
+// than 512 candidates goes to the general path.
+template <int NCH, bool VEC, bool GREEDY, bool CMODE, bool BIGK>
+__device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>& L) {
+  constexpr uint32_t kEnt = FastLds<NCH, BIGK>::kEnt;
+  static_assert(sizeof(FastLds<NCH, BIGK>) <= 160u * 1024u, "LDS");
   static_assert(NCH * 4 <= 32, "slot masks are 32 bits");
   typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -819,9 +885,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     const uint64_t m = __ballot(hit);
     if (m) {
       const uint32_t o = nent + lanes_below(m);
-      if (hit && o < kEntries) {
-        L.ent[wave * kEntries + o] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
-        L.etag[wave * kEntries + o] = chunk_pos<NCH>((uint32_t)c, wave, lane) | ((uint32_t)c << 28);
+      if (hit && o < kEnt) {
+        L.ent[wave * kEnt + o] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
+        L.etag[wave * kEnt + o] = chunk_pos<NCH>((uint32_t)c, wave, lane) | ((uint32_t)c << 28);
       }
       nent += (uint32_t)__popcll((unsigned long long)m);
     }
@@ -840,7 +906,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
   uint32_t pmv = 0u;
   uint32_t slot_n = kCandN, slot_o = kOverflow;  // the pass's candidate count and overflow flag
   auto settle = [&]() __attribute__((always_inline)) {
-    if (__builtin_expect(nent > kEntries, 0)) {
+    if (__builtin_expect(nent > kEnt, 0)) {
       if (lane == 0) atomicOr(&L.misc[slot_o], 1u);
       return;
     }
@@ -849,8 +915,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       float4 ev = make_float4(0.f, 0.f, 0.f, 0.f);
       uint32_t tag = 0u;
       if (k < nent) {
-        ev = L.ent[wave * kEntries + k];
-        tag = L.etag[wave * kEntries + k];
+        ev = L.ent[wave * kEnt + k];
+        tag = L.etag[wave * kEnt + k];
       }
       const uint32_t base = tag & 0x00ffffffu, c = tag >> 28;
       uint32_t rem = k < nent ? ((ev.x >= tf ? 1u : 0u) | (ev.y >= tf ? 2u : 0u) | (ev.z >= tf ? 4u : 0u) |
@@ -929,19 +995,24 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       LLMHIP_NOTE(15, n);
     }
   }
-  if (__builtin_expect(!spec || n < K || n > kFastCand || ovf, 0)) {
+  // The small-K kernel ranks at most 512 candidates.
+  const uint32_t ncap = BIGK ? kFastCand : 512u;
+  if (__builtin_expect(!spec || n < K || n > ncap || ovf, 0)) {
     LLMHIP_NOTE(13, spec ? 1u : 2u);
     // The proven threshold. Known values are those of the slots outside the
     // history and the mask: final without a penalty, which (rp >= 1) only
     // lowers a value. t0 is the lower edge of the fine bin holding the K-th
-    // largest of the 1024 per-thread known maxima, so at least K known
-    // values lie at or above it, and a history slot can reach it only if
-    // its raw value does. The scan and settle run again at t0 (lowered past
+    // largest of the 1024 per-thread known maxima (or per-chunk maxima), so
+    // at least K known values lie at or above it, and a history slot can
+    // reach it only if its raw value does. The scan and settle run again at t0 (lowered past
     // ties after the division by T): at least K candidates. Everyone is past
     // the sample histogram and the scan entries, so their LDS is reused.
     const uint32_t pmr = cmode && use_pen ? table_bits() : pmv;
     const uint32_t known = ~(pmr | mkbits);
-    const float tm = known_max(pmr);
+    // A large K takes the K-th largest of the 8192 per-chunk known maxima
+    // instead: 1024 per-thread maxima put far more than K values above
+    // their K-th largest when K is a large share of 1024.
+    const bool by_chunk = BIGK && K > kSpecMaxK;
     reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
     lds_barrier();  // every wave has read the candidate count and overflow flag above
@@ -952,10 +1023,26 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     }
     slot_n = kCandN;
     slot_o = kOverflow;
-    if (tm > -INFINITY) {
-      const uint32_t k = f2key(tm);
-      atomicAdd(&L.coarse[k >> 24], 1u);
-      atomicAdd(&L.fine[k >> 20], 1u);
+    if (by_chunk) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        float cm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if ((known >> (4 * c + j)) & 1u) cm = fmaxf(cm, x[4 * c + j]);
+        if (cm > -INFINITY) {
+          const uint32_t k = f2key(cm);
+          atomicAdd(&L.coarse[k >> 24], 1u);
+          atomicAdd(&L.fine[k >> 20], 1u);
+        }
+      }
+    } else {
+      const float tm = known_max(pmr);
+      if (tm > -INFINITY) {
+        const uint32_t k = f2key(tm);
+        atomicAdd(&L.coarse[k >> 24], 1u);
+        atomicAdd(&L.fine[k >> 20], 1u);
+      }
     }
     lds_barrier();
     // A finite maximum's key is at least 0x00800000, above -inf's and NaN's
@@ -976,7 +1063,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     lds_barrier();
     LLMHIP_MARK(13);
     n = L.misc[kCandN];
-    if (__builtin_expect(n > kFastCand || L.misc[kOverflow], 0)) {
+    if (__builtin_expect(n > ncap || L.misc[kOverflow] != 0u, 0)) {
       // Too many values at or above the threshold for the scan entries or
       // the list (a large K): narrow it per slot. Level 1: the fine bin
       // holding the K-th largest known value at or above it (tk0 <= t0, so
@@ -984,8 +1071,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       // crowded: 12 more key bits inside it. At least K final values lie at
       // or above the result.
       LLMHIP_NOTE(13, 3u);
-      uint32_t* fine1 = reinterpret_cast<uint32_t*>(L.ent);  // kWaves * kEntries float4 >= kFineBins words
-      uint32_t* coarse1 = L.etag;                              // kWaves * kEntries words >= kCoarseBins
+      uint32_t* fine1 = reinterpret_cast<uint32_t*>(L.ent);  // kWaves * kEnt float4 >= kFineBins words
+      uint32_t* coarse1 = L.etag;                              // kWaves * kEnt words >= kCoarseBins
       reinterpret_cast<uint4*>(fine1)[tid] = make_uint4(0u, 0u, 0u, 0u);
       if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(coarse1)[tid] = make_uint4(0u, 0u, 0u, 0u);
       lds_barrier();  // every wave has read the count and flag, and is past the entries
@@ -1025,9 +1112,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       if (tkey == 0u) return false;
       LLMHIP_MARK(14);
       tf = key2f(tkey);
-      // Every lane appends its own final values at or above the threshold,
-      // one ballot per slot, with no scan entries (so no per-wave region can
-      // overflow).
 #pragma unroll
       for (int e = 0; e < NCH * 4; ++e) {
         const uint32_t pos = chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3);
@@ -1050,7 +1134,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
       n = L.misc[kCandN];
     }
     // Heavy ties or an unusually flat top: not bounded by the register path.
-    if (n < K || n > kFastCand) return false;
+    if (n < K || n > ncap) return false;
   }
 
   // 6. Ranks by (w key desc, id asc).
@@ -1061,10 +1145,11 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
     rank_in_regs<3>(L.ord, n, K, wave, lane, L.skey, L.sid);
   } else if (n <= 256) {
     rank_in_regs<4>(L.ord, n, K, wave, lane, L.skey, L.sid);
-  } else if (n <= 512) {
+  } else if (!BIGK) {
+    if (n > 512u) return false;
     rank_in_regs<8>(L.ord, n, K, wave, lane, L.skey, L.sid);
   } else {
-    rank_in_lds(L.ord, n, K, L.skey, L.sid);
+    rank_in_lds(L.ord, reinterpret_cast<uint64_t*>(L.ent), n, K, L.skey, L.sid);  // the entries are consumed
   }
   LLMHIP_MARK(10);
   lds_barrier();
@@ -1072,7 +1157,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH>& L) {
 
   // 7. The sequential tail (one wave).
   if (wave == 0) {
-    if (__builtin_expect(K <= 64, 1)) {
+    if (!BIGK || K <= 64u) {
       draw_tail_bcast(a, b, len_b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u,
                       u_draw, st_next, L.exptab, L.tail);
     } else {

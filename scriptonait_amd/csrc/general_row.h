@@ -135,6 +135,10 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
 // ---------------------------------------------------------------------------
 // counts_moved: the row's count table (decode-step mode with counts) was
 // already moved to this step's window by the kernel that handed it over.
+// SORT = false leaves out the whole-row sort, for the register path's
+// hand-overs: those are greedy rows and top-k rows with K <= 1024, which
+// select in LDS (K <= kSelCap), and the kernel is 20 KB of code smaller.
+template <bool SORT = true>
 __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, GenLds& L, bool counts_moved) {
   const llmhip_params P = load_params(a, b);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -236,6 +240,7 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
     }
     return;
   }
+  if constexpr (!SORT) return;  // not reached: see above
 
   // Stable LSD radix sort, 4 x 8-bit digits, descending: ties keep
   // ascending id, which is the reference's order (generate.rs:364-367).

@@ -24,8 +24,8 @@
 static __device__ __align__(256) uint32_t scratch[LLMHIP_NOALLOC_SCRATCH_BYTES / sizeof(uint32_t)];
 
 namespace llmhip {
-hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s);
-hipError_t launch_fast_counts(const SampleArgs& a, bool vec, hipStream_t s);
+hipError_t launch_fast(const SampleArgs& a, bool vec, bool bigk, hipStream_t s);
+hipError_t launch_fast_counts(const SampleArgs& a, bool vec, bool bigk, hipStream_t s);
 hipError_t launch_general(const SampleArgs& a, hipStream_t s);
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
@@ -222,10 +222,12 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
     return LLMHIP_OK;
   }
   uint32_t classes = 0;
-  if (params_stride == 0) {
-    classes = row_class(params_host[0], (uint32_t)V);
-  } else {
-    for (size_t b = 0; b < B; ++b) classes |= row_class(params_host[b * params_stride], (uint32_t)V);
+  bool bigk = false;  // some top-k row of the register path has K > 64
+  for (size_t b = 0; b < (params_stride ? B : 1); ++b) {
+    const llmhip_params& p = params_host[b * params_stride];
+    const uint32_t c = row_class(p, (uint32_t)V);
+    classes |= c;
+    bigk = bigk || (c == kClassTopK && p.top_k > 64u);
   }
   const bool fast_ok = V <= kMaxFastV;
   const uint32_t fast_mask = fast_ok ? (classes & (kClassGreedy | kClassTopK)) : 0u;
@@ -295,7 +297,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
       a.slotmask = sm;
     }
     a.row_class_mask = fast_mask;
-    HIP_TRY(a.counts ? launch_fast_counts(a, vec, s) : launch_fast(a, vec, s));
+    HIP_TRY(a.counts ? launch_fast_counts(a, vec, bigk, s) : launch_fast(a, vec, bigk, s));
   }
   if (vocab_mask) {
     a.row_class_mask = vocab_mask;

@@ -126,7 +126,9 @@ hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s) {
 }
 
 // Calls without a count table (decode steps with one: fast_counts.hip).
-hipError_t launch_fast(const SampleArgs& a, bool vec, hipStream_t s) { return launch_fast_mode<false>(a, vec, s); }
+hipError_t launch_fast(const SampleArgs& a, bool vec, bool bigk, hipStream_t s) {
+  return launch_fast_mode<false>(a, vec, bigk, s);
+}
 
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(sample_vocab_kernel, dim3(a.B), dim3(kBlock), 0, s, a);
