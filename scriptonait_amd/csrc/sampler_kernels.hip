@@ -50,6 +50,7 @@ __global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
     __syncthreads();
     general_row(a, b, L.gen, true);
   }
+  LLMHIP_MARK(11);
 }
 
 // ---------------------------------------------------------------------------

@@ -476,6 +476,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
   };
   classify(0, fs[0], kVB, 0.0, kVBeyond0);
   __syncthreads();
+  LLMHIP_MARK(NF == 1 ? 3 : 7);
   const uint32_t kb0 = L.misc[kVBeyond0];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -645,6 +646,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
   nin = wave_sum(nin);
   if (lane == 0) atomicAdd(&L.misc[kVCount], nin);
   __syncthreads();
+  LLMHIP_MARK(NF == 1 ? 4 : 8);
   const uint32_t nt = L.misc[kVNTies];
   if (L.misc[kVFail] || nt > kVTies) return false;
 
@@ -784,6 +786,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
     lds_signal(&L.misc[kVSplitDone]);
   }
 
+  LLMHIP_MARK(NF == 1 ? 5 : 9);
   // Replays (wave 0), one fold after the other: certain segments as
   // integers, tie zones split at their ties, gathering zones 64 elements at a
   // time.
@@ -1004,6 +1007,7 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
   keep_out = L.misc[kVKeep];
   const bool ok = L.misc[kVFail] == 0u;
   __syncthreads();
+  LLMHIP_MARK(NF == 1 ? 6 : 10);
   return ok;
 }
 
@@ -1033,6 +1037,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   mx = L.redf[0];
   for (uint32_t w = 1; w < kWaves; ++w) mx = fmaxf(mx, L.redf[w]);
   if (L.misc[kVFail] || mx == -INFINITY) return false;
+  LLMHIP_MARK(1);
 
   // Bucket counts and approximate masses. The masses add up as integers
   // (x in units of 2^-40): LDS integer atomics are much faster than float ones.
@@ -1063,6 +1068,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   __syncthreads();
   for (uint32_t k = tid; k < kVB; k += kBlock) L.asum[k] = (float)((double)amass[k] * 0x1p-40);
   __syncthreads();
+  LLMHIP_MARK(2);
 
   // generate.rs:372-377: the softmax sum. The max element has x = 1, so S >= 1.
   const uint32_t ncand = L.misc[kVCand];
@@ -1133,6 +1139,7 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
 // Returns false (uniformly) when the row must go to general_row.
 __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, VocabLds& L, bool vec4) {
   const uint32_t tid = threadIdx.x;
+  LLMHIP_MARK(0);
   const llmhip_params P = load_params(a, b);
   const uint32_t V = a.V;
   const float* row = a.logits + (size_t)b * a.ld;
