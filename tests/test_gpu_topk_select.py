@@ -99,3 +99,19 @@ def test_exact_ties_in_the_lds_tail_folds(sampler, K):
     assert np.array_equal(g.kept, o.kept)
     assert np.array_equal(g.rng_state, o.rng_state)
     assert np.array_equal(g.probs, o.probs)
+
+
+@pytest.mark.parametrize("k", [65, 300, 700, 1024, 2000, 4096])
+def test_lds_tail_sum_is_the_reference_fold(sampler, k):
+    """The LDS tail folds the softmax sum 64 terms at a time in integer ulps
+    (a binade at a time, ties and binade changes stepped in f32). Every
+    probability is e_i / sum, so with top_p = 1 and min_p = 0 (all K kept)
+    the probabilities must equal the oracle's bit for bit, not just within
+    the tolerance: one ulp off in the sum would show in every one of them."""
+    w = make_workload(3, B=24)
+    for T in (0.7, 1.0, 3.0):
+        prm = make_params(T, k, 1.0, 0.0, 1.15)
+        g, o = run_both(sampler, w, params=prm)
+        assert np.array_equal(g.ids, o.ids)
+        assert np.array_equal(g.kept, o.kept)
+        assert np.array_equal(g.probs.view(np.uint32), o.probs.view(np.uint32)), f"k={k} T={T}"
