@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_len=None, max_prompt=300,
-         eos_rows=1, counts=False):
+         eos_rows=1, counts=False, fixed=0.0):
     import torch
 
     from oracle import oracle
@@ -53,8 +53,16 @@ def _run(sampler, V, prm, steps=24, B=16, window=128, cap=256, seed=3, context_l
     resets = 0
     done = np.zeros(B, dtype=bool)
     st = rng0.copy()
+    # fixed > 0: every step's logits are one fixed row plus `fixed` times fresh
+    # noise, so the generation draws the same top ids again and again and
+    # the window fills with the row's own best candidates (the penalty then
+    # pushes them below the register path's speculative threshold).
+    base = rs.standard_normal((B, V)) * 3.0 if fixed else None
     for t in range(steps):
-        logits = (rs.standard_normal((B, V)) * 3.0).astype(np.float32)
+        if fixed:
+            logits = (base + fixed * rs.standard_normal((B, V))).astype(np.float32)
+        else:
+            logits = (rs.standard_normal((B, V)) * 3.0).astype(np.float32)
         for b in range(0, B, eos_rows):  # some rows end at EOS along the way
             if (b + 3 * t) % 29 == 0:
                 logits[b, EOS_ID] = 60.0
@@ -163,6 +171,29 @@ def test_decode_loop_with_count_table(sampler, path):
         _run(sampler, 2048, make_params(1.0, 0, 0.9, 0.02, 1.8), window=16, cap=17, counts=True)
     else:
         _run(sampler, 8192, make_params(0.0, 64, 0.95, 0.05, 1.3), counts=True)
+
+
+@pytest.mark.parametrize("k", [64, 300, 700])
+@pytest.mark.parametrize("counts", [False, True])
+def test_decode_loop_drawing_its_own_top_ids(sampler, k, counts):
+    """Logits that barely change from step to step: the window fills with
+    the rows' own top candidates, so the register path's retries (a second
+    speculative pass, the proven threshold from per-thread or per-chunk
+    known maxima) and, with a count table, its table reads for those
+    retries run at every step. Ids, rings and RNG states match the CPU loop
+    step by step."""
+    _run(sampler, 32000, make_params(0.8, k, 0.97, 0.0, 1.3), steps=40, B=16, window=256, cap=320,
+         max_prompt=50, counts=counts, fixed=0.3, eos_rows=4)
+
+
+def test_decode_loop_greedy_drawing_its_own_top_ids(sampler):
+    """Greedy rows whose window holds their own argmax again and again: the
+    penalty bound (only history slots at or above the largest known value
+    are penalized) must still give the reference's argmax."""
+    _run(sampler, 32000, make_params(0.0, 64, 0.95, 0.05, 1.05), steps=40, B=16, window=256, cap=320,
+         max_prompt=50, fixed=0.3, eos_rows=4)
+    _run(sampler, 32000, make_params(0.0, 64, 0.95, 0.05, 1.05), steps=40, B=16, window=256, cap=320,
+         max_prompt=50, fixed=0.3, counts=True, eos_rows=4)
 
 
 def test_decode_loop_with_count_table_and_cache_resets(sampler):
