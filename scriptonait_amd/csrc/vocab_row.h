@@ -1013,18 +1013,27 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
 
 // The three folds and the draw, given the row's source. Returns false
 // (uniformly) when the row must go to general_row.
-template <class Src>
+// raw: the same row before the division by T, and div_T that T (> 0,
+// finite, normal) when the max pass may read it instead (else 0): w -> w / T
+// rounded is monotone, so the largest quotient is the largest value's, and
+// one division replaces one per element.
+template <class Src, class RawSrc>
 __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uint32_t len_b, const llmhip_params& P, VocabLds& L,
-                            const Src& src) {
+                            const Src& src, const RawSrc& raw, float div_T) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t V = a.V;
   // Max; NaN and +inf rows take the sorting path.
   float mx = -INFINITY;
   uint32_t bad = 0u;
-  src.for_each([&](float w, uint32_t) __attribute__((always_inline)) {
+  auto max_of = [&](float w, uint32_t) __attribute__((always_inline)) {
     if (w != w || w == INFINITY) bad = 1u;
     mx = fmaxf(mx, w);
-  });
+  };
+  if (div_T > 0.0f) {
+    raw.for_each(max_of);
+  } else {
+    src.for_each(max_of);
+  }
 #pragma unroll
   for (uint32_t off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   if (__ballot(bad != 0u) && lane == 0) L.misc[kVFail] = 1u;
@@ -1036,7 +1045,8 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   __syncthreads();
   mx = L.redf[0];
   for (uint32_t w = 1; w < kWaves; ++w) mx = fmaxf(mx, L.redf[w]);
-  if (L.misc[kVFail] || mx == -INFINITY) return false;
+  if (div_T > 0.0f) mx = mx / div_T;  // generate.rs:357-359 for the largest value
+  if (L.misc[kVFail] || mx == -INFINITY || mx == INFINITY) return false;
   LLMHIP_MARK(1);
 
   // Bucket counts and approximate masses. The masses add up as integers
@@ -1213,7 +1223,7 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   const uint32_t* allowed_bits = a.allowed_bits;
   const uint32_t allowed_len = a.allowed_len, eos = a.eos_id;
   const bool div_t = T != 1.0f;
-  auto wval = [allowed, allowed_bits, allowed_len, eos, &L, use_pen, div_t, T](uint32_t i, float v)
+  auto wraw = [allowed, allowed_bits, allowed_len, eos, &L, use_pen](uint32_t i, float v)
       __attribute__((always_inline)) -> float {
     if (allowed) {  // generate.rs:333-341
       if (i < allowed_len && i != eos && allowed[i] == 0) v = -INFINITY;
@@ -1235,11 +1245,17 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
         }
       }
     }
+    return v;
+  };
+  auto wval = [wraw, div_t, T](uint32_t i, float v) __attribute__((always_inline)) -> float {
+    v = wraw(i, v);
     if (div_t) v = v / T;  // generate.rs:357-359
     return v;
   };
   const StreamSrc<decltype(wval)> src{row, V, vec4, wval};
-  return vocab_folds(a, b, len_b, P, L, src);
+  const StreamSrc<decltype(wraw)> raw{row, V, vec4, wraw};
+  const bool defer = div_t && T >= 0x1p-126f && T < INFINITY;
+  return vocab_folds(a, b, len_b, P, L, src, raw, defer ? T : 0.0f);
 }
 
 }  // namespace llmhip
