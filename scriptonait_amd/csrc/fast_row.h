@@ -963,12 +963,17 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
   LLMHIP_NOTE(12, n);
   // A speculative threshold the penalty undercut (a history holding the
   // row's own top ids): once more from the sample histogram, at a position
-  // deeper by the factor the settle fell short of 5K/4 (at most 8). One
-  // wave selects it (a selection in every wave would compete for the ALUs).
+  // deep enough for the 5K/4 - n survivors still missing (at most 8 times
+  // the first). One wave selects it (a selection in every wave would compete
+  // for the ALUs).
   if (__builtin_expect(spec && n < K && !ovf, 0)) {
     if (wave == 0u) {
       const uint64_t q = spec_q();
-      const uint64_t want = n ? (q * 5u * K + 4u * n - 1u) / (4u * n) : 8u * q;
+      // q sample positions stand for (kSpecNum/kSpecDen)*K values; the
+      // values below the first threshold are assumed to survive the penalty
+      // two times in three, so 3/2 * (5K/4 - n) more of them are wanted.
+      const uint64_t need = 5u * K / 4u - n;  // n < K
+      const uint64_t want = q + (q * need * 3u * kSpecDen + 2u * kSpecNum * K - 1u) / (2u * kSpecNum * K);
       const uint64_t q2 = want < 8u * q ? want : 8u * q;
       const uint32_t tk2 = lower_past_ties(hist_select(L.coarse, L.fine, (uint32_t)q2, false, lane), T, lane);
       (void)lds_publish(&L.misc[kTau2], tk2 != 0u && key2f(tk2) < tf ? tk2 : 1u);
