@@ -26,23 +26,34 @@
 
 namespace llmhip {
 
+// generate.rs:372-373: buf[i] = expf(w_i - max) for the n sorted
+// candidates (the max is the first key, or -inf when the keys are NaN), and
+// +0.0 up to n rounded to 64. Threads first, first + stride, ... share it.
+template <class KeyAt>
+__device__ __forceinline__ void stage_exp_terms(float* buf, uint32_t n, KeyAt key_at, const uint64_t* tab,
+                                                uint32_t first, uint32_t stride) {
+  const uint32_t k0 = key_at(0);
+  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
+  const uint32_t nr = (n + 63u) & ~63u;
+  for (uint32_t i = first; i < nr; i += stride) buf[i] = i < n ? glibc_expf_tab(key2f(key_at(i)) - mx, tab) : 0.0f;
+}
+
 // The same computation for n <= 4096 candidates, with the terms staged in
-// LDS (`buf`: n rounded up to 64 floats, 16-byte aligned). Every fold is the
+// LDS (`buf`: n rounded up to 64 floats, 16-byte aligned; STAGED: the
+// caller has staged them, by stage_exp_terms). Every fold is the
 // reference's left fold in f32, read as broadcast float4s: the softmax sum
 // 16 terms per step, top-p and the walk in blocks of 8 whose last value is
 // tested (c never decreases; r - p < 0 exactly when r < p), the block that
 // decides being resolved once, one lane per term. Terms past the kept
 // prefix are set to +0.0, which leaves either fold unchanged.
 // Must be called by all 64 lanes of exactly one wave.
-template <class KeyAt, class IdAt>
+template <bool STAGED = false, class KeyAt, class IdAt>
 __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, uint32_t len_b, const llmhip_params& P,
                                               uint32_t n, KeyAt key_at, IdAt id_at, uint64_t st, const uint64_t* tab,
                                               float* buf) {
   const uint32_t lane = lane_id();
-  const uint32_t k0 = key_at(0);
-  const float mx = k0 <= kKeyNaN ? -INFINITY : key2f(k0);
   const uint32_t nr = (n + 63u) & ~63u;
-  for (uint32_t i = lane; i < nr; i += 64u) buf[i] = i < n ? glibc_expf_tab(key2f(key_at(i)) - mx, tab) : 0.0f;
+  if (!STAGED) stage_exp_terms(buf, n, key_at, tab, lane, 64u);
   const float4* b4 = reinterpret_cast<const float4*>(buf);
   auto t8_at = [&](uint32_t base, float (&t8)[8]) __attribute__((always_inline)) {
     const float4 lo = b4[base / 4u], hi = b4[base / 4u + 1u];
@@ -79,21 +90,29 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
     }
     return;
   }
-  for (uint32_t i = lane; i < n; i += 64u) buf[i] = buf[i] / sum;  // generate.rs:378-380
-
-  // generate.rs:384-395: longest prefix with p >= min_p * p_0, at least 1.
+  // generate.rs:378-380: p_i = e_i / sum, and generate.rs:384-395: the
+  // longest prefix with p >= min_p * p_0, at least 1. With min-p, p_i is
+  // computed only as far as that prefix reaches: the terms past it are
+  // cleared below.
   uint32_t keep = n;
   if (P.min_p > 0.0f) {
-    const float thr = P.min_p * buf[0];
+    const float thr = P.min_p * (buf[0] / sum);
     for (uint32_t c = 0; c < n; c += 64u) {
       const uint32_t i = c + lane;
-      const uint64_t fail = __ballot(i < n && !(buf[i] >= thr));
+      float p = 0.0f;
+      if (i < n) {
+        p = buf[i] / sum;
+        buf[i] = p;
+      }
+      const uint64_t fail = __ballot(i < n && !(p >= thr));
       if (fail) {
         keep = c + (uint32_t)__ffsll((unsigned long long)fail) - 1u;
         break;
       }
     }
     if (keep < 1u) keep = 1u;
+  } else {
+    for (uint32_t i = lane; i < n; i += 64u) buf[i] = buf[i] / sum;
   }
   for (uint32_t i = keep + lane; i < nr; i += 64u) buf[i] = 0.0f;
 

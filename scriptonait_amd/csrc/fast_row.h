@@ -1,5 +1,5 @@
 // Register path of the gfx950 sampler: one row per 1024-thread workgroup,
-// V <= 32768, 0 < top_k <= 1024 (and greedy rows).
+// V <= 32768, 0 < top_k <= 4096 (and greedy rows).
 //
 // Row semantics: crates/llm-core/src/generate.rs:325-420. The row is read
 // once from HBM into registers, all of it at once (the memory queues run
@@ -36,6 +36,7 @@
 // mask and penalty was at or above it before. Rows with p < 1 (or NaN) take
 // the general path.
 #pragma once
+#include <cstddef>
 #include <type_traits>
 
 #include "draw_tail.h"
@@ -74,6 +75,8 @@ constexpr uint32_t kTauWaves = 8;                 // waves whose maxima form the
 constexpr uint32_t kSpecNum = 8, kSpecDen = 5;    // the threshold aims at ~(kSpecNum/kSpecDen)*K values
 constexpr uint32_t kSpecMaxK = 384;               // larger K: the scan entries would overflow; proven threshold
 constexpr uint32_t kRefineCount = 16;             // a fine bin holding more keys is split once more
+constexpr uint32_t kSortedK = 1024;               // K up to which the sorted top K is copied to skey/sid
+constexpr uint32_t kBigCand = 7168;               // K > kSortedK: candidates per row (the scan entries' LDS)
 
 // misc[] slots
 constexpr int kSyncSample = 0;  // waves whose sample is in the histogram
@@ -92,12 +95,16 @@ constexpr int kTau0 = 13;      // the proven threshold key (1: not bounded here)
 
 // BIGK: the large-K kernel's scan entries hold 128 per wave (a proven
 // threshold for K up to 1024 puts about 1.2 K chunks in them).
+// K > kSortedK: the candidate list takes the LDS of the scan entries
+// (ent, etag and ord, which are contiguous), and its sort ping-pongs with
+// big_tmp, which the count table's LDS holds once the penalties are applied.
 template <int NCH, bool BIGK = false>
 struct FastLds {
   static constexpr uint32_t kEnt = BIGK ? 128u : kEntries;
   union {
     uint32_t cnt[NCH * 2048];  // u16 history multiplicities, two per word (V <= NCH*4096)
     GenLds gen;                // the general path's LDS when a row falls back
+    uint64_t big_tmp[BIGK ? kBigCand : 1];
   };
   uint32_t pm[kBlock];  // per-thread mask: slot is penalized
   __attribute__((aligned(16))) uint32_t coarse[kCoarseBins];
@@ -105,14 +112,25 @@ struct FastLds {
   float4 ent[kWaves * kEnt];  // scan entries: a lane's 4 values of a chunk with a hit
   __attribute__((aligned(16))) uint32_t etag[kWaves * kEnt];  // chunk position | chunk << 28
   __attribute__((aligned(16))) uint64_t ord[kFastCand];  // settled order keys; then the tail's terms
-  uint32_t skey[kMaxFastK];  // sorted top-K: post-temperature key
-  uint32_t sid[kMaxFastK];   //               id
+  uint32_t skey[kSortedK];  // sorted top-K: post-temperature key
+  uint32_t sid[kSortedK];   //               id
   uint64_t exptab[32];
   __attribute__((aligned(16))) float tail[128];
   float redv[kWaves];
   uint32_t redi[kWaves];
   uint32_t misc[16];
 };
+
+// The large-K candidate list: kBigCand order keys over ent, etag and ord.
+template <int NCH>
+__device__ __forceinline__ uint64_t* big_list(FastLds<NCH, true>& L) {
+  using F = FastLds<NCH, true>;
+  static_assert(offsetof(F, etag) == offsetof(F, ent) + sizeof(L.ent) &&
+                    offsetof(F, ord) == offsetof(F, etag) + sizeof(L.etag) &&
+                    sizeof(L.ent) + sizeof(L.etag) + sizeof(L.ord) >= kBigCand * sizeof(uint64_t),
+                "ent, etag and ord hold the large-K list");
+  return reinterpret_cast<uint64_t*>(L.ent);
+}
 
 // Read-only inputs that every lane of a wave reads at the same address go
 // through the constant address space, so they become scalar (SMEM) loads:
@@ -332,6 +350,20 @@ __device__ __forceinline__ HistPos hist_locate(const uint32_t* coarse, const uin
   return HistPos{(cb * 16u + 15u - fl) << 20, cnt, need - (readlane_u32(fi, fl) - cnt)};
 }
 
+// The coarse histogram as sums of the fine one (coarse bin c = fine bins
+// 16c .. 16c+15), for histograms counted into fine bins only: their keys
+// crowd a few coarse bins, whose atomics would serialize. All threads; a
+// barrier must follow before hist_locate reads it.
+__device__ __forceinline__ void coarse_from_fine(const uint32_t* fine, uint32_t* coarse) {
+  static_assert(kFineBins == 4u * kBlock && kFineBins == 16u * kCoarseBins, "one uint4 per thread");
+  const uint32_t tid = threadIdx.x;
+  const uint4 q = reinterpret_cast<const uint4*>(fine)[tid];
+  uint32_t v = q.x + q.y + q.z + q.w;
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  if ((tid & 3u) == 0u) coarse[tid >> 2] = v;
+}
+
 // The Q-th largest key counted in the histogram, as a key threshold. exact:
 // the lower edge of the fine bin holding it, so at least Q counted keys lie
 // at or above the result. Otherwise an estimate inside that bin, taking its
@@ -421,32 +453,20 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t* v, uint32_t n) {
   }
 }
 
-// First index j in [lo, hi) of a descending run with v[j] < x (strict) or
-// v[j] <= x: the number of the run's keys above x (or at or above it) is
-// j - lo. About log2(hi - lo) + 1 LDS reads.
-__device__ __forceinline__ uint32_t desc_bound(const uint64_t* v, uint32_t lo, uint32_t hi, uint64_t x, bool strict) {
-  while (lo < hi) {
-    const uint32_t mid = (lo + hi) >> 1;
-    const uint64_t m = v[mid];
-    if (strict ? m >= x : m > x) {
-      lo = mid + 1u;
-    } else {
-      hi = mid;
-    }
-  }
-  return lo;
-}
-
-// More candidates than the register ranks hold (n <= kFastCand): sort them,
-// descending. Runs of 64 keys are sorted in registers, one key per lane, by
-// a bitonic network of lane exchanges (no barrier); then runs are merged in
-// pairs, log2(n / 64) rounds between v and tmp with one barrier each: a key's
-// place in the merged run is its index in its own run plus its rank in the
-// other run, found by binary search (keys of the first run go before equal
-// keys of the second, which only the zero padding has). The K best are
-// written to skey/sid in sorted order.
-__device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint64_t* tmp, uint32_t n, uint32_t K, uint32_t* skey,
-                                            uint32_t* sid) {
+// Sorts the n order keys in ord[] descending (all threads of the
+// workgroup; ord and tmp hold n rounded up to 64 entries). Runs of 64 keys
+// are sorted in registers, one key per lane, by a bitonic network of lane
+// exchanges (no barrier); then runs are merged in pairs, log2(n / 64)
+// rounds between ord and tmp with one barrier each. In a round, thread t
+// writes the E merged keys at positions tE .. tE+E-1 (E * 1024 >= n and E a
+// power of two, so they lie in one pair of runs A, B): a binary search along
+// its diagonal of the merge (the merge path) finds how many of the keys
+// before them come from A, then E steps merge from the two heads. A key of
+// A goes before an equal key of B (only the zero padding has equal keys).
+// Returns the buffer that holds the sorted keys (ord or tmp), past a
+// barrier.
+template <int E>
+__device__ __forceinline__ uint64_t* sort_desc_lds(uint64_t* ord, uint64_t* tmp, uint32_t n) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t np = (n + 63u) & ~63u;
   for (uint32_t r = wave; r * 64u < np; r += kWaves) {
@@ -464,25 +484,57 @@ __device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint64_t* tmp, uint32
   lds_barrier();
   uint64_t* src = ord;
   uint64_t* dst = tmp;
+  const uint32_t g = tid * (uint32_t)E;  // this thread's first output position
   for (uint32_t R = 64u; R < np; R <<= 1) {
-    for (uint32_t i = tid; i < np; i += kBlock) {
-      const uint32_t s0 = i & ~(2u * R - 1u);
-      const uint32_t a1 = min(s0 + R, np), b1 = min(s0 + 2u * R, np);
-      const uint64_t x = src[i];
-      uint32_t at;
-      if (i < a1) {  // first run: the second run's keys above x come first
-        at = i + (desc_bound(src, a1, b1, x, false) - a1);
-      } else {       // second run: the first run's keys at or above x come first
-        at = (i - a1) + desc_bound(src, s0, a1, x, true);
+    if (g < np) {
+      const uint32_t s0 = g & ~(2u * R - 1u);
+      const uint32_t la = min(R, np - s0), lb = min(2u * R, np - s0) - la;
+      const uint64_t* A = src + s0;
+      const uint64_t* B = A + la;
+      const uint32_t d = g - s0;
+      // The first d outputs are A[0, i) and B[0, d - i): i is the first
+      // index whose A key does not go before B[d - i - 1].
+      uint32_t lo = d > lb ? d - lb : 0u, hi = min(d, la);
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (A[mid] >= B[d - mid - 1u]) {
+          lo = mid + 1u;
+        } else {
+          hi = mid;
+        }
       }
-      dst[at] = x;
+      uint32_t ia = lo, jb = d - lo;
+      uint64_t ha = ia < la ? A[ia] : 0ull, hb = jb < lb ? B[jb] : 0ull;
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        const bool take_a = jb >= lb || (ia < la && ha >= hb);
+        dst[g + (uint32_t)k] = take_a ? ha : hb;
+        if (k + 1 < E) {
+          if (take_a) {
+            ++ia;
+            ha = ia < la ? A[ia] : 0ull;
+          } else {
+            ++jb;
+            hb = jb < lb ? B[jb] : 0ull;
+          }
+        }
+      }
     }
     lds_barrier();
     uint64_t* t = src;
     src = dst;
     dst = t;
   }
-  for (uint32_t i = tid; i < K; i += kBlock) {
+  return src;
+}
+
+// More candidates than the register ranks hold (n <= kFastCand): sort them
+// and write the K best to skey/sid in sorted order.
+__device__ __forceinline__ void rank_in_lds(uint64_t* ord, uint64_t* tmp, uint32_t n, uint32_t K, uint32_t* skey,
+                                            uint32_t* sid) {
+  static_assert(kFastCand <= 2u * kBlock, "two keys per thread");
+  const uint64_t* src = n <= kBlock ? sort_desc_lds<1>(ord, tmp, n) : sort_desc_lds<2>(ord, tmp, n);
+  for (uint32_t i = threadIdx.x; i < K; i += kBlock) {
     const uint64_t o = src[i];
     skey[i] = (uint32_t)(o >> 32);
     sid[i] = 0xffffffffu - (uint32_t)o;
@@ -663,6 +715,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
     return false;
   }
   const uint32_t K = P.top_k;  // 0 < K < V, K <= kMaxFastK unless greedy (row class)
+  // More than skey/sid hold: the candidates are listed over the scan
+  // entries' LDS, sorted there, and the tail reads the K best in place.
+  const bool huge = BIGK && K > kSortedK;
 
   // Multiplicity of position p in the window. Positions past V (padding
   // slots) have none, and the table holds no word for them.
@@ -1018,8 +1073,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
     // instead: 1024 per-thread maxima put far more than K values above
     // their K-th largest when K is a large share of 1024.
     const bool by_chunk = BIGK && K > kSpecMaxK;
+    // The histograms below count into fine bins only (coarse_from_fine).
     reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
     lds_barrier();  // every wave has read the candidate count and overflow flag above
     LLMHIP_MARK(11);
     if (tid == 0) {
@@ -1035,40 +1090,40 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if ((known >> (4 * c + j)) & 1u) cm = fmaxf(cm, x[4 * c + j]);
-        if (cm > -INFINITY) {
-          const uint32_t k = f2key(cm);
-          atomicAdd(&L.coarse[k >> 24], 1u);
-          atomicAdd(&L.fine[k >> 20], 1u);
-        }
+        if (cm > -INFINITY) atomicAdd(&L.fine[f2key(cm) >> 20], 1u);
       }
     } else {
       const float tm = known_max(pmr);
-      if (tm > -INFINITY) {
-        const uint32_t k = f2key(tm);
-        atomicAdd(&L.coarse[k >> 24], 1u);
-        atomicAdd(&L.fine[k >> 20], 1u);
-      }
+      if (tm > -INFINITY) atomicAdd(&L.fine[f2key(tm) >> 20], 1u);
     }
+    lds_barrier();
+    coarse_from_fine(L.fine, L.coarse);
     lds_barrier();
     // A finite maximum's key is at least 0x00800000, above -inf's and NaN's
     // (hist_locate's 0 says fewer than K threads hold a known value).
     if (wave == 0u) {
       const uint32_t t0 = hist_locate(L.coarse, L.fine, K, lane).lo;
-      const uint32_t tk = t0 ? lower_past_ties(t0, T, lane) : 0u;
+      // A large K goes to the per-slot narrowing below, which needs only
+      // some key at or below its K-th largest known value: t0, or, when
+      // fewer than K chunks hold a known value, the lowest finite key.
+      const uint32_t tk = huge ? (t0 ? t0 : 0x00800000u) : t0 ? lower_past_ties(t0, T, lane) : 0u;
       (void)lds_publish(&L.misc[kTau0], tk ? tk : 1u);
     }
     const uint32_t tk0 = lds_wait_nonzero(&L.misc[kTau0], 1u, a);
     if (tk0 <= 1u) return false;
     LLMHIP_MARK(12);
     tf = key2f(tk0);
-    nent = 0u;
+    // A large K puts more values at or above t0 than the scan entries hold.
+    if (!huge) {
+      nent = 0u;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) scan_chunk(c, mc[c]);
-    settle();
-    lds_barrier();
-    LLMHIP_MARK(13);
-    n = L.misc[kCandN];
-    if (__builtin_expect(n > ncap || L.misc[kOverflow] != 0u, 0)) {
+      for (int c = 0; c < NCH; ++c) scan_chunk(c, mc[c]);
+      settle();
+      lds_barrier();
+      LLMHIP_MARK(13);
+      n = L.misc[kCandN];
+    }
+    if (__builtin_expect(huge || n > ncap || L.misc[kOverflow] != 0u, 0)) {
       // Too many values at or above the threshold for the scan entries or
       // the list (a large K): narrow it per slot. Level 1: the fine bin
       // holding the K-th largest known value at or above it (tk0 <= t0, so
@@ -1079,37 +1134,38 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
       uint32_t* fine1 = reinterpret_cast<uint32_t*>(L.ent);  // kWaves * kEnt float4 >= kFineBins words
       uint32_t* coarse1 = L.etag;                              // kWaves * kEnt words >= kCoarseBins
       reinterpret_cast<uint4*>(fine1)[tid] = make_uint4(0u, 0u, 0u, 0u);
-      if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(coarse1)[tid] = make_uint4(0u, 0u, 0u, 0u);
       lds_barrier();  // every wave has read the count and flag, and is past the entries
       if (tid == 0) {
         L.misc[kCandN] = 0u;
         L.misc[kOverflow] = 0u;
       }
+      // (A fresh copy of the mask per loop: shared between the loops, its 32
+      // per-slot bits would stay live in registers from one to the next.)
+      uint32_t kn1 = known;
+      asm volatile("" : "+v"(kn1));
 #pragma unroll
       for (int e = 0; e < NCH * 4; ++e) {
         const uint32_t k = f2key(x[e]);
-        if (((known >> e) & 1u) && k >= tk0) {
-          atomicAdd(&coarse1[k >> 24], 1u);
-          atomicAdd(&fine1[k >> 20], 1u);
-        }
+        if (((kn1 >> e) & 1u) && k >= tk0) atomicAdd(&fine1[k >> 20], 1u);
       }
       lds_barrier();  // level 1 counted; every wave is past level 0's reads
+      coarse_from_fine(fine1, coarse1);
+      lds_barrier();
       const HistPos h1 = hist_locate(coarse1, fine1, K, lane);
       LLMHIP_NOTE(14, h1.cnt);
       uint32_t thr = h1.lo;
       if (h1.cnt > kRefineCount) {
         reinterpret_cast<uint4*>(L.fine)[tid] = make_uint4(0u, 0u, 0u, 0u);
-        if (tid < kCoarseBins / 4) reinterpret_cast<uint4*>(L.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);
         lds_barrier();
+        uint32_t kn2 = known;
+        asm volatile("" : "+v"(kn2));
 #pragma unroll
         for (int e = 0; e < NCH * 4; ++e) {
           const uint32_t k = f2key(x[e]);
-          if (((known >> e) & 1u) && (k >> 20) == (h1.lo >> 20)) {
-            const uint32_t k2 = k << 12;
-            atomicAdd(&L.coarse[k2 >> 24], 1u);
-            atomicAdd(&L.fine[k2 >> 20], 1u);
-          }
+          if (((kn2 >> e) & 1u) && (k >> 20) == (h1.lo >> 20)) atomicAdd(&L.fine[(k << 12) >> 20], 1u);
         }
+        lds_barrier();
+        coarse_from_fine(L.fine, L.coarse);
         lds_barrier();
         thr = h1.lo | (hist_locate(L.coarse, L.fine, h1.need, lane).lo >> 12);
       }
@@ -1117,33 +1173,87 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
       if (tkey == 0u) return false;
       LLMHIP_MARK(14);
       tf = key2f(tkey);
+      uint64_t* list = L.ord;
+      uint32_t lcap = kFastCand;
+      if constexpr (BIGK) {
+        if (huge) {
+          lds_barrier();  // every wave is past the level-1 bins, which the list overwrites
+          list = big_list(L);
+          lcap = kBigCand;
+        }
+      }
+      // Every thread's final values at or above the threshold, then their
+      // places in the list from a scan of the per-thread counts (a counter
+      // in LDS would serialize the waves' appends, one per slot).
+      uint32_t hits = 0u;
 #pragma unroll
       for (int e = 0; e < NCH * 4; ++e) {
-        const uint32_t pos = chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3);
         float v = x[e];
         bool ok = v >= tf && ((mkbits >> e) & 1u) == 0u;
         if (ok && ((pmr >> e) & 1u)) {
-          v = apply_penalty(v, count_of(pos), rp);
+          v = apply_penalty(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3)), rp);
           ok = v >= tf;
         }
-        const uint64_t mk = __ballot(ok);
-        if (mk) {
-          uint32_t o = 0u;
-          if (lane == 0) o = atomicAdd(&L.misc[kCandN], (uint32_t)__popcll((unsigned long long)mk));
-          o = readlane_u32(o, 0) + lanes_below(mk);
-          if (ok && o < kFastCand) L.ord[o] = cand_order(f2key(v / T), pos);
+        x[e] = v;
+        hits |= (ok ? 1u : 0u) << e;
+      }
+      const uint32_t hc = (uint32_t)__popc(hits);
+      const uint32_t hinc = wave_incl_scan(hc);
+      if (lane == 63u) L.redi[wave] = hinc;
+      lds_barrier();
+      uint32_t o = hinc - hc, total = 0u;
+#pragma unroll
+      for (uint32_t w = 0; w < kWaves; ++w) {
+        const uint32_t t = L.redi[w];
+        o += w < wave ? t : 0u;
+        total += t;
+      }
+      // Listed as (value bits, position) first: the division by T is then
+      // made once per listed value, spread over all threads, instead of by
+      // every wave for each slot where one of its lanes has a hit.
+#pragma unroll
+      for (int e = 0; e < NCH * 4; ++e) {
+        if ((hits >> e) & 1u) {
+          const uint32_t pos = chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3);
+          if (o < lcap) list[o] = ((uint64_t)__float_as_uint(x[e]) << 32) | pos;
+          ++o;
         }
       }
       lds_barrier();
+      for (uint32_t i = tid; i < min(total, lcap); i += kBlock) {
+        const uint64_t r = list[i];
+        list[i] = cand_order(f2key(__uint_as_float((uint32_t)(r >> 32)) / T), (uint32_t)r);
+      }
+      lds_barrier();
       LLMHIP_MARK(15);
-      n = L.misc[kCandN];
+      n = total;
     }
     // Heavy ties or an unusually flat top: not bounded by the register path.
-    if (n < K || n > ncap) return false;
+    if (n < K || n > (huge ? kBigCand : ncap)) return false;
   }
 
   // 6. Ranks by (w key desc, id asc).
   LLMHIP_MARK(9);
+  if constexpr (BIGK) {
+    if (huge) {
+      // The list sorted in LDS (the count table's LDS is free once every
+      // penalty is applied); the tail stages its terms in the other buffer.
+      static_assert(kBigCand <= 8u * kBlock, "eight keys per thread");
+      uint64_t* lst = big_list(L);
+      const uint64_t* srt = n <= 2u * kBlock   ? sort_desc_lds<2>(lst, L.big_tmp, n)
+                            : n <= 4u * kBlock ? sort_desc_lds<4>(lst, L.big_tmp, n)
+                                               : sort_desc_lds<8>(lst, L.big_tmp, n);
+      float* buf = srt == L.big_tmp ? reinterpret_cast<float*>(big_list(L)) : reinterpret_cast<float*>(L.big_tmp);
+      auto key_at = [&](uint32_t i) { return (uint32_t)(srt[i] >> 32); };
+      // The tail's terms are staged by every wave.
+      stage_exp_terms(buf, K, key_at, L.exptab, tid, kBlock);
+      lds_barrier();
+      if (wave == 0)
+        draw_tail_lds<true>(a, b, len_b, P, K, key_at, [&](uint32_t i) { return ~(uint32_t)srt[i]; }, rng0, L.exptab,
+                            buf);
+      return true;
+    }
+  }
   if (n <= 128) {
     rank_in_regs<2>(L.ord, n, K, wave, lane, L.skey, L.sid);
   } else if (n <= 192) {
@@ -1160,14 +1270,19 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
   lds_barrier();
   LLMHIP_MARK(7);
 
-  // 7. The sequential tail (one wave).
+  // 7. The sequential tail (one wave). For K > 64 every wave stages its
+  //    terms first (the candidate list's LDS is free past the rank).
+  if (BIGK && K > 64u) {
+    stage_exp_terms(reinterpret_cast<float*>(L.ord), K, [&](uint32_t i) { return L.skey[i]; }, L.exptab, tid, kBlock);
+    lds_barrier();
+  }
   if (wave == 0) {
     if (!BIGK || K <= 64u) {
       draw_tail_bcast(a, b, len_b, P, K, lane < K ? L.skey[lane] : kKeyNone, lane < K ? L.sid[lane] : 0u,
                       u_draw, st_next, L.exptab, L.tail);
     } else {
-      draw_tail_lds(a, b, len_b, P, K, [&](uint32_t i) { return L.skey[i]; }, [&](uint32_t i) { return L.sid[i]; },
-                    rng0, L.exptab, reinterpret_cast<float*>(L.ord));
+      draw_tail_lds<true>(a, b, len_b, P, K, [&](uint32_t i) { return L.skey[i]; },
+                          [&](uint32_t i) { return L.sid[i]; }, rng0, L.exptab, reinterpret_cast<float*>(L.ord));
     }
   }
   LLMHIP_MARK(8);

@@ -289,7 +289,7 @@ constexpr uint32_t kStatusWords = 4;
 
 constexpr uint32_t kBlock = 1024;
 constexpr uint32_t kWaves = kBlock / 64;
-constexpr uint32_t kMaxFastK = 1024;     // largest top_k of the register path
+constexpr uint32_t kMaxFastK = 4096;     // largest top_k of the register path
 constexpr uint32_t kMaxFastV = 32768;    // largest V of the register path
 
 // Chunks per lane of the fast kernel for a vocabulary of V (V <= kMaxFastV):

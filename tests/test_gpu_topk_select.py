@@ -1,8 +1,9 @@
-"""GPU: top-k rows of the sorting path against the oracle.
+"""GPU: top-k rows beyond the headline K against the oracle.
 
-Rows with 1024 < top_k <= 4096 (and rows the fast kernel hands over) select
-the K largest keys by a radix select and sort them in LDS; larger K sort the
-whole row in HBM scratch. Both must give the reference's order: key
+Rows with 64 < top_k <= 4096 and V <= 32768 stay in the fast kernel's
+large-K variant. Rows it hands over (and larger V) select the K largest keys
+by a radix select in the sorting path and sort them in LDS; K > 4096 sorts
+the whole row in HBM scratch. All must give the reference's order: key
 descending, ties by ascending id (crates/llm-core/src/generate.rs:364-367).
 """
 import numpy as np
@@ -61,6 +62,23 @@ def test_top_k_select_other_vocab_sizes(sampler, V, k):
     compare(g, o, f"V={V} k={k}")
 
 
+@pytest.mark.parametrize("k", [1025, 2000, 3000, 4096])
+@pytest.mark.parametrize("filters", [(0.7, 0.95, 0.05, 1.15), (1.0, 1.0, 0.0, 1.0), (0.9, 0.9, 0.0, 1.3)])
+def test_register_path_k_above_1024(sampler, k, filters):
+    """1024 < K <= 4096 stays in the fast kernel: the threshold is narrowed
+    per slot to the K-th largest known value, the candidates are listed over
+    the scan entries' LDS and merge-sorted there, and the tail's terms are
+    staged by every wave. Ids, kept counts, probabilities and RNG states
+    match the oracle, and no row is handed to the sorting path."""
+    T, top_p, min_p, rp = filters
+    w = make_workload(3, B=32)
+    prm = make_params(T, k, top_p, min_p, rp)
+    sampler.status()  # clears the hand-over count
+    g, o = run_both(sampler, w, params=prm)
+    assert sampler.status().handovers == 0
+    compare(g, o, f"k={k} filters={filters}")
+
+
 @pytest.mark.parametrize("k", [65, 128, 700, 1024])
 @pytest.mark.parametrize("filters", [(0.7, 0.95, 0.05, 1.15), (1.0, 1.0, 0.0, 1.0)])
 def test_fast_kernel_k_above_64(sampler, k, filters):
@@ -103,11 +121,11 @@ def test_exact_ties_in_the_lds_tail_folds(sampler, K):
 
 @pytest.mark.parametrize("k", [65, 300, 700, 1024, 2000, 4096])
 def test_lds_tail_sum_is_the_reference_fold(sampler, k):
-    """The LDS tail folds the softmax sum 64 terms at a time in integer ulps
-    (a binade at a time, ties and binade changes stepped in f32). Every
-    probability is e_i / sum, so with top_p = 1 and min_p = 0 (all K kept)
-    the probabilities must equal the oracle's bit for bit, not just within
-    the tolerance: one ulp off in the sum would show in every one of them."""
+    """The LDS tail folds the softmax sum term by term in f32, in sorted
+    order. Every probability is e_i / sum, so with top_p = 1 and min_p = 0
+    (all K kept) the probabilities must equal the oracle's bit for bit, not
+    just within the tolerance: one ulp off in the sum would show in every
+    one of them."""
     w = make_workload(3, B=24)
     for T in (0.7, 1.0, 3.0):
         prm = make_params(T, k, 1.0, 0.0, 1.15)
