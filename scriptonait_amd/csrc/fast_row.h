@@ -879,8 +879,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
   // The sample position the speculative threshold takes: the target
   // (kSpecNum/kSpecDen)*K scaled to the positions the sample holds.
   auto spec_q = [&]() __attribute__((always_inline)) {
-    const uint64_t sampled = L.misc[kSampled];
-    return (uint32_t)(((uint64_t)kSpecNum * K * sampled + (uint64_t)kSpecDen * V - 1u) / ((uint64_t)kSpecDen * V)) + 2u;
+    // In 32 bits: sampled <= kTauWaves * 2048 and K <= kMaxFastK.
+    static_assert((uint64_t)kSpecNum * kMaxFastK * kTauWaves * 2048u + kSpecDen * kMaxFastV < (1ull << 32), "fits");
+    const uint32_t sampled = L.misc[kSampled];
+    return (kSpecNum * K * sampled + kSpecDen * V - 1u) / (kSpecDen * V) + 2u;
   };
   // 2. The first kTauWaves waves to get here put their sample maxima in the
   //    histogram, and the last of them selects the speculative threshold:
