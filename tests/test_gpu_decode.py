@@ -173,7 +173,7 @@ def test_decode_loop_with_count_table(sampler, path):
         _run(sampler, 8192, make_params(0.0, 64, 0.95, 0.05, 1.3), counts=True)
 
 
-@pytest.mark.parametrize("k", [64, 300, 700])
+@pytest.mark.parametrize("k", [64, 300, 700, 2000])
 @pytest.mark.parametrize("counts", [False, True])
 def test_decode_loop_drawing_its_own_top_ids(sampler, k, counts):
     """Logits that barely change from step to step: the window fills with

@@ -79,6 +79,23 @@ def test_register_path_k_above_1024(sampler, k, filters):
     compare(g, o, f"k={k} filters={filters}")
 
 
+@pytest.mark.parametrize("k", [350, 512, 2000])
+def test_register_path_retries_with_a_mask_and_penalty(sampler, k):
+    """K = 350 / 512 take the proven threshold (the speculative one is not
+    used past K = 384, or undercut) and K = 2000 the per-slot narrowing, here
+    with a mask that disallows a tenth of the ids and a penalty of 1.3 over
+    the history: masked and penalized slots are not known values, so the
+    threshold must come from the others. Every row matches the oracle and
+    none is handed to the sorting path."""
+    w = make_workload(3, B=32)
+    allowed = (np.random.default_rng(k).random(w.V) >= 0.1).astype(np.uint8)
+    prm = make_params(0.8, k, 0.97, 0.01, 1.3)
+    sampler.status()  # clears the hand-over count
+    g, o = run_both(sampler, w, params=prm, allowed=allowed)
+    assert sampler.status().handovers == 0
+    compare(g, o, f"k={k} masked, rp=1.3")
+
+
 @pytest.mark.parametrize("k", [65, 128, 700, 1024])
 @pytest.mark.parametrize("filters", [(0.7, 0.95, 0.05, 1.15), (1.0, 1.0, 0.0, 1.0)])
 def test_fast_kernel_k_above_64(sampler, k, filters):
