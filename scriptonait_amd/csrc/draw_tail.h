@@ -61,15 +61,15 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
     t8[4] = hi.x; t8[5] = hi.y; t8[6] = hi.z; t8[7] = hi.w;
   };
 
-  // generate.rs:374: sum = ((0 + e_0) + e_1) + ..., the next 16 terms
-  // loading while the current 16 are added.
+  // generate.rs:374: sum = ((0 + e_0) + e_1) + ... . Term by term over the
+  // float4s [q0, q1) (a multiple of 4 apart), the next 16 terms loading while
+  // the current 16 are added.
   float sum = 0.0f;
-  {
-    const uint32_t nq = nr / 4u;
-    float4 c0 = b4[0], c1 = b4[1], c2 = b4[2], c3 = b4[3];
-    for (uint32_t q = 0; q < nq; q += 4u) {
+  auto add_terms = [&](uint32_t q0, uint32_t q1) __attribute__((always_inline)) {
+    float4 c0 = b4[q0], c1 = b4[q0 + 1u], c2 = b4[q0 + 2u], c3 = b4[q0 + 3u];
+    for (uint32_t q = q0; q < q1; q += 4u) {
       float4 d0 = c0, d1 = c1, d2 = c2, d3 = c3;
-      if (q + 4u < nq) {
+      if (q + 4u < q1) {
         d0 = b4[q + 4u];
         d1 = b4[q + 5u];
         d2 = b4[q + 6u];
@@ -81,6 +81,30 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
       sum += c3.x; sum += c3.y; sum += c3.z; sum += c3.w;
       c0 = d0; c1 = d1; c2 = d2; c3 = d3;
     }
+  };
+  // The first 64 terms one at a time (the sum passes through its first
+  // binades there). Then 64 at a time: while the sum S stays in its binade
+  // [2^E, 2^(E+1)), fl(S + t) = S + rne(t / u) * u with u = 2^(E-23), an
+  // integer count of ulps that does not depend on S, except at an exact
+  // half-ulp tie, where round-half-even looks at S's last bit. A block with
+  // no such tie whose counts keep S in its binade adds their total at once
+  // (exact: S / u + total < 2^24); any other block (a binade change, a tie, a
+  // term or sum that is not finite) is added term by term.
+  add_terms(0u, min(nr, 64u) / 4u);
+  for (uint32_t base = 64u; base < nr; base += 64u) {
+    const float t = buf[base + lane];
+    bool step = !(sum >= 1.0f) || !isfinite(sum);
+    if (!step) {
+      const int E = (int)((__float_as_uint(sum) >> 23) & 0xffu) - 127;  // sum is normal, >= 1
+      const float q = ldexpf(t, 23 - E);                                 // t / u, exact
+      const float r = rintf(q);
+      const bool odd = !isfinite(t) || q - floorf(q) == 0.5f;
+      const uint32_t tot = readlane_u32(wave_incl_scan((uint32_t)r), 63u);
+      const uint32_t si = (uint32_t)ldexpf(sum, 23 - E);  // S / u, in [2^23, 2^24)
+      step = __ballot(odd) != 0ull || si + tot >= (1u << 24);
+      if (!step) sum = ldexpf((float)(si + tot), E - 23);
+    }
+    if (step) add_terms(base / 4u, base / 4u + 16u);
   }
   // generate.rs:375-377: degenerate exit, no draw.
   if (!(sum > 0.0f) || !isfinite(sum)) {
