@@ -140,12 +140,21 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
   }
   for (uint32_t i = keep + lane; i < nr; i += 64u) buf[i] = 0.0f;
 
+  // The top-p and walk folds below run 64 terms at a time in integer ulps
+  // where they can, as the softmax sum does: inside a binade and with no
+  // half-ulp tie, each step adds (or subtracts) rne(p / u) ulps, so a wave
+  // scan of those counts gives every running value of the block exactly.
+  // A block where that does not hold runs term by term.
+  auto ulp_exp = [](float x) __attribute__((always_inline)) {  // x normal: x in [2^E, 2^(E+1))
+    return (int)((__float_as_uint(x) >> 23) & 0xffu) - 127;
+  };
+
   // generate.rs:397-411: c_i = ((0 + p_0) + ...) + p_i; the cut is the first
   // c_i >= top_p (all of the prefix when top_p >= 1 or never reached); the
   // total is the fold at the last kept term.
   uint32_t stop = keep;
-  float total;
-  {
+  float total = 0.0f;
+  if (__builtin_expect(keep <= 64u, 1)) {  // one block: term by term, in a compact loop
     const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
     float c = 0.0f, cprev = 0.0f;
     uint32_t k8 = 0u;
@@ -166,6 +175,62 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
     const uint64_t hit = __ballot(lane < 8u && k8 + lane < keep && t >= tp);
     if (hit) stop = k8 + (uint32_t)__ffsll((unsigned long long)hit);
     total = readlane_f32(t, stop - 1u - k8);
+  } else {
+    const float tp = P.top_p < 1.0f ? P.top_p : INFINITY;
+    float c = 0.0f;
+    bool done = false;
+    // Term by term over [b0, b0 + 64): blocks of 8 whose last value is
+    // tested; the block with the cut (or with the end of the kept prefix) is
+    // resolved by lanes j < 8, each recomputing c_{base+j} from its start.
+    auto fold_terms = [&](uint32_t b0) __attribute__((always_inline)) {
+      for (uint32_t base = b0; base < b0 + 64u; base += 8u) {
+        float t8[8];
+        t8_at(base, t8);
+        const float cprev = c;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c += t8[j];
+        if (c >= tp || base + 8u >= keep) {
+          float t = cprev;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) t = (uint32_t)j <= lane ? t + t8[j] : t;
+          const uint64_t hit = __ballot(lane < 8u && base + lane < keep && t >= tp);
+          stop = hit ? base + (uint32_t)__ffsll((unsigned long long)hit) : keep;
+          total = readlane_f32(t, stop - 1u - base);
+          done = true;
+          return;
+        }
+      }
+    };
+    const uint32_t kr = (keep + 63u) & ~63u;
+    for (uint32_t b0 = 0u; b0 < kr && !done; b0 += 64u) {
+      // The first block term by term (c starts at 0 and climbs through
+      // binades), and a block with few kept terms left (a scan costs about
+      // as much as 30 steps).
+      bool step = b0 == 0u || keep - b0 < 32u || !(c >= 0x1p-126f) || !isfinite(c);
+      if (!step) {
+        const float pj = buf[b0 + lane];  // 0 past keep
+        const int E = ulp_exp(c);
+        const float q = ldexpf(pj, 23 - E);  // p / u, exact (p <= p_0 <= c)
+        const float rq = rintf(q);
+        const uint32_t P = wave_incl_scan((uint32_t)rq);
+        const uint32_t ci = (uint32_t)ldexpf(c, 23 - E);  // c / u, in [2^23, 2^24)
+        step = __ballot(q - floorf(q) == 0.5f) != 0ull || ci + readlane_u32(P, 63u) >= (1u << 24);
+        if (!step) {
+          const float cj = ldexpf((float)(ci + P), E - 23);  // c after term b0 + lane
+          const uint64_t hit = __ballot(b0 + lane < keep && cj >= tp);
+          if (hit) {
+            const uint32_t j = (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+            stop = b0 + j + 1u;
+            total = readlane_f32(cj, j);
+            done = true;
+          } else {
+            c = readlane_f32(cj, 63u);
+          }
+        }
+      }
+      if (step) fold_terms(b0);
+    }
+    if (!done) total = c;  // the kept prefix ended in a block added in ulps
   }
   // Terms past the cut leave the walk's r unchanged too.
   for (uint32_t i = stop + lane; i < keep; i += 64u) buf[i] = 0.0f;
@@ -174,7 +239,7 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
   // subtracts p_i; no hit picks the last kept term.
   const float u = next_f32(st);
   uint32_t pick = stop - 1u;
-  {
+  if (__builtin_expect(stop <= 64u, 1)) {  // one block: term by term, in a compact loop
     float r = u * total, rprev = r;
     uint32_t k8 = 0u;
     bool neg = false;
@@ -199,6 +264,68 @@ __device__ __forceinline__ void draw_tail_lds(const SampleArgs& a, uint32_t b, u
       const float pj = lane < 8u ? buf[k8 + lane] : 0.0f;
       const uint64_t hit = __ballot(lane < 8u && k8 + lane < stop && t < pj);
       if (hit) pick = k8 + (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+    }
+  } else {
+    float r = u * total;
+    bool found = false;
+    // Term by term over [b0, b0 + 64): blocks of 8 whose last value is tested
+    // (r_i - p_i < 0 exactly when r_i < p_i), the deciding block resolved by
+    // lanes j < 8, each recomputing r_{base+j} before its own subtraction.
+    auto walk_terms = [&](uint32_t b0) __attribute__((always_inline)) {
+      for (uint32_t base = b0; base < b0 + 64u && base < stop; base += 8u) {
+        float t8[8];
+        t8_at(base, t8);
+        const float rprev = r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r -= t8[j];
+        if (r < 0.0f) {
+          float t = rprev;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) t = (uint32_t)j < lane ? t - t8[j] : t;
+          const float pj = lane < 8u ? buf[base + lane] : 0.0f;
+          const uint64_t hit = __ballot(lane < 8u && base + lane < stop && t < pj);
+          if (hit) pick = base + (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+          found = true;
+          return;
+        }
+      }
+    };
+    const uint32_t sr = (stop + 63u) & ~63u;
+    for (uint32_t b0 = 0u; b0 < sr && !found; b0 += 64u) {
+      // Term by term: the first block of a short walk (it usually ends
+      // there), and a block with few terms left.
+      bool step = (b0 == 0u && stop <= 256u) || stop - b0 < 32u || !(r >= 0x1p-126f) || !isfinite(r);
+      if (!step) {
+        const float pj = buf[b0 + lane];  // 0 past stop
+        const int E = ulp_exp(r);
+        const float q = ldexpf(pj, 23 - E);
+        // p can exceed r by far here (the pick): counts of 2^25 and more are
+        // clamped, which keeps the scan from wrapping; every lane after such
+        // a term fails the bound below, and its own test hits.
+        const float rq = rintf(fminf(q, 0x1p25f));
+        const uint32_t qi = (uint32_t)rq;
+        const uint32_t Pi = wave_incl_scan(qi), Pe = Pi - qi;
+        const uint32_t ri = (uint32_t)ldexpf(r, 23 - E);  // r / u, in [2^23, 2^24)
+        const uint64_t ties = __ballot(q - floorf(q) == 0.5f);
+        // r before lane j's test is exact while no tie comes before j and
+        // every value so far stays a whole ulp above 2^E (below it the
+        // spacing halves): the lanes where that holds are a prefix [0, v).
+        const bool ok = (ties & lanemask_lt()) == 0ull && Pe < ri - (1u << 23);
+        const uint64_t okm = __ballot(ok);
+        const uint32_t v = okm == ~0ull ? 64u : (uint32_t)__ffsll((unsigned long long)~okm) - 1u;
+        const float rb = ldexpf((float)(ri - Pe), E - 23);
+        const uint64_t hit = __ballot(lane < v && b0 + lane < stop && rb < pj);
+        const uint32_t tot = readlane_u32(Pi, 63u);
+        if (hit) {
+          pick = b0 + (uint32_t)__ffsll((unsigned long long)hit) - 1u;
+          found = true;
+        } else if (v == 64u && ties == 0ull && tot < ri - (1u << 23)) {
+          r = ldexpf((float)(ri - tot), E - 23);
+        } else {
+          step = true;
+        }
+      }
+      if (step) walk_terms(b0);
     }
   }
   if (lane == 0) {
