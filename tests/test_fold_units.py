@@ -1,5 +1,6 @@
 """The two facts the full-vocabulary kernel (scriptonait_amd/csrc/vocab_row.h)
-rests on, checked on the CPU.
+and the LDS tail's block folds (scriptonait_amd/csrc/draw_tail.h) rest on,
+checked on the CPU.
 
 1. x = expf(w - max) is monotone: glibc's expf is non-decreasing over every
    binary32 input in [-104, 0] (below that it is 0). With w - max and p = x / S
@@ -127,3 +128,21 @@ def test_a_fold_of_one_binade_is_order_free_apart_from_ties():
             continue
         Mn = M + q[rs.permutation(t.size)].sum()
         assert np.float32(np.ldexp(float(Mn), int(E) - 23)) == F
+
+
+def test_a_subtraction_that_lands_on_the_binade_floor_can_round_below_it():
+    """Why the walk's integer steps need their result a whole ulp above 2^E
+    (M - q > 2^23, as `_check` and the LDS tail's walk require): with
+    F = 2^E + u and t between u and 1.5 u, rne(t / u) = 1 puts the rule's
+    result on 2^E exactly, but F - t lies below 2^E, where the spacing is
+    u / 2, and rounds to 2^E - u / 2 once it is closer to that."""
+    E = np.arange(-20, 20)
+    u = np.ldexp(1.0, E - 23)
+    F = np.ldexp(float((1 << 23) + 1), E - 23).astype(np.float32)
+    t = (1.4 * u).astype(np.float32)
+    _, Mn = _fold_step(F, t, sub=True)
+    assert (Mn == (1 << 23)).all()  # the rule lands on 2^E ...
+    ref = (F - t).astype(np.float32)
+    assert (ref == (np.ldexp(1.0, E) - u / 2).astype(np.float32)).all()  # ... f32 rounds below it
+    inside, _, _ = _check(F, t, sub=True)
+    assert not inside.any()
