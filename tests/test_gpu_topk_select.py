@@ -136,6 +136,20 @@ def test_exact_ties_in_the_lds_tail_folds(sampler, K):
     assert np.array_equal(g.probs, o.probs)
 
 
+@pytest.mark.parametrize("k", [2, 9, 40, 64])
+def test_register_tail_sum_is_the_reference_fold(sampler, k):
+    """K <= 64: the register tail's softmax sum, bit for bit (every
+    probability is e_i / sum, all K kept with top_p = 1 and min_p = 0), at
+    temperatures that put the sum in one binade or across several."""
+    w = make_workload(3, B=32)
+    for T in (0.05, 0.7, 1.0, 3.0, 30.0):
+        prm = make_params(T, k, 1.0, 0.0, 1.15)
+        g, o = run_both(sampler, w, params=prm)
+        assert np.array_equal(g.ids, o.ids)
+        assert np.array_equal(g.kept, o.kept)
+        assert np.array_equal(g.probs.view(np.uint32), o.probs.view(np.uint32)), f"k={k} T={T}"
+
+
 @pytest.mark.parametrize("k", [65, 300, 700, 1024, 2000, 4096])
 def test_lds_tail_sum_is_the_reference_fold(sampler, k):
     """The LDS tail folds the softmax sum term by term in f32, in sorted
