@@ -1137,10 +1137,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
       uint32_t* coarse1 = L.etag;                              // kWaves * kEnt words >= kCoarseBins
       reinterpret_cast<uint4*>(fine1)[tid] = make_uint4(0u, 0u, 0u, 0u);
       lds_barrier();  // every wave has read the count and flag, and is past the entries
-      if (tid == 0) {
-        L.misc[kCandN] = 0u;
-        L.misc[kOverflow] = 0u;
-      }
       // (A fresh copy of the mask per loop: shared between the loops, its 32
       // per-slot bits would stay live in registers from one to the next.)
       uint32_t kn1 = known;
