@@ -81,23 +81,28 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   uint32_t t, r;
   select_kth(keys, V, K, L, t, r);
-  // Every key above t goes to [0, K - r) in any order (the sort below
-  // orders them); thread tid walks ids [tid*S, tid*S + S) and counts its
-  // keys equal to t.
+  // Wave w walks the ids [w*R, (w+1)*R) in steps of 64 consecutive ids, 8
+  // steps in flight: every load is coalesced, and each wave meets its ids
+  // in ascending order. The keys above t (exactly K - r of them) go to
+  // [0, K - r) in any order (the sort below orders them); the keys equal to
+  // t are counted per wave.
   if (tid == 0) L.sv[2] = 0u;
   __syncthreads();
-  const uint32_t S = (V + kBlock - 1u) / kBlock;
-  const uint32_t i0 = tid * S, i1 = min(V, i0 + S);
-  uint32_t ties = 0u;
-  for (uint32_t j0 = 0; j0 < S; j0 += 8u) {
+  const uint32_t R = ((V + kWaves - 1u) / kWaves + 63u) & ~63u;
+  const uint32_t w0 = wave * R, w1 = min(V, w0 + R);
+  uint32_t ties = 0u;  // this wave's keys equal to t
+  for (uint32_t j0 = w0; j0 < w1; j0 += 8u * 64u) {
     uint32_t kb[8];
 #pragma unroll
-    for (uint32_t u = 0; u < 8u; ++u) kb[u] = i0 + j0 + u < i1 ? keys[i0 + j0 + u] : 0u;
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t i = j0 + u * 64u + lane;
+      kb[u] = i < w1 ? keys[i] : 0u;
+    }
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
-      const uint32_t i = i0 + j0 + u, k = kb[u];
-      const bool above = i < i1 && k > t;
-      ties += (i < i1 && k == t) ? 1u : 0u;
+      const uint32_t i = j0 + u * 64u + lane, k = kb[u];
+      const bool above = i < w1 && k > t;
+      ties += (uint32_t)__popcll((unsigned long long)__ballot(i < w1 && k == t));
       const uint64_t m = __ballot(above);
       if (m) {
         uint32_t o = 0u;
@@ -107,20 +112,23 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
       }
     }
   }
-  // The r lowest ids among the keys equal to t: a block scan of the
-  // per-thread counts (threads hold ascending id ranges) places them at
-  // [K - r, K).
-  const uint32_t winc = wave_incl_scan(ties);
-  if (lane == 63u) L.bins[wave] = winc;
+  if (lane == 0) L.redi[wave] = ties;
   __syncthreads();
-  uint32_t rank = winc - ties;
-  for (uint32_t w = 0; w < wave; ++w) rank += L.bins[w];
+  // The r lowest ids among the keys equal to t go to [K - r, K): the waves'
+  // ranges are in id order, so a key's place among them is the ties of the
+  // waves before its own, then of its wave's earlier steps and lanes.
+  uint32_t rank = 0u;
+  for (uint32_t w = 0; w < wave; ++w) rank += L.redi[w];
   if (ties != 0u && rank < r) {
-    for (uint32_t i = i0; i < i1 && rank < r; ++i) {
-      if (keys[i] == t) {
-        L.sel[K - r + rank] = sel_order(t, i);
-        ++rank;
+    for (uint32_t j0 = w0; j0 < w1 && rank < r; j0 += 64u) {
+      const uint32_t i = j0 + lane;
+      const bool tie = i < w1 && keys[i] == t;
+      const uint64_t m = __ballot(tie);
+      if (tie) {
+        const uint32_t q = rank + lanes_below(m);
+        if (q < r) L.sel[K - r + q] = sel_order(t, i);
       }
+      rank += (uint32_t)__popcll((unsigned long long)m);
     }
   }
   bitonic_sort_desc(L.sel, K);  // its first barrier completes the list

@@ -23,15 +23,16 @@ def test_top_k_above_the_fast_limit(sampler, k):
     compare(g, o, f"k={k}")
 
 
-@pytest.mark.parametrize("k", [1100, 3000])
-def test_top_k_select_with_ties_at_the_cut(sampler, k):
+@pytest.mark.parametrize("V,k", [(32000, 1100), (32000, 3000), (40000, 50), (40000, 1100), (40000, 3000)])
+def test_top_k_select_with_ties_at_the_cut(sampler, V, k):
     """Logits on a coarse grid: the K-th key is shared by hundreds of ids, of
-    which only the lowest ids are kept."""
-    w = make_workload(3, B=16)
+    which only the lowest ids are kept (V = 40000: the sorting path's LDS
+    select, whose waves meet their ids in ascending order)."""
+    w = make_workload(3, B=16, V=V)
     w.logits[:] = np.round(w.logits * 2.0) / 2.0
     prm = make_params(1.3, k, 1.0, 0.0, 1.0)
     g, o = run_both(sampler, w, params=prm)
-    compare(g, o, f"quantized k={k}")
+    compare(g, o, f"quantized V={V} k={k}")
 
 
 def test_top_k_select_fewer_allowed_than_k(sampler):
