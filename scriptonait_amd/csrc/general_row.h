@@ -134,6 +134,57 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
   bitonic_sort_desc(L.sel, K);  // its first barrier completes the list
 }
 
+// select_top for keys taken before the division by T (keys[i] = f2key(v_i)):
+// division is monotone, so every value of the top K after it (ties by id)
+// lies at or above tlo, the lowest raw key whose quotient equals that of the
+// K-th largest raw key, and only those values are divided. When tlo is not
+// bounded (a tie run longer than 64 keys, or a K-th value at -inf or NaN)
+// or the candidates outnumber the list, every key is divided in place and
+// select_top runs on them.
+__device__ __forceinline__ void select_top_raw(uint32_t* keys, uint32_t V, uint32_t K, float T, GenLds& L) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  uint32_t t, r;
+  select_kth(keys, V, K, L, t, r);
+  const uint32_t tlo = lower_past_ties(t, T, lane);  // the same in every wave
+  uint32_t c = 0u;
+  if (tlo != 0u) {
+    if (tid == 0) L.sv[2] = 0u;
+    __syncthreads();
+    // Coalesced, as in select_top: wave w walks ids [w*R, (w+1)*R).
+    const uint32_t R = ((V + kWaves - 1u) / kWaves + 63u) & ~63u;
+    const uint32_t w0 = wave * R, w1 = min(V, w0 + R);
+    for (uint32_t j0 = w0; j0 < w1; j0 += 8u * 64u) {
+      uint32_t kb[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t i = j0 + u * 64u + lane;
+        kb[u] = i < w1 ? keys[i] : 0u;
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t i = j0 + u * 64u + lane, k = kb[u];
+        const bool cand = i < w1 && k >= tlo;
+        const uint64_t m = __ballot(cand);
+        if (m) {
+          uint32_t o = 0u;
+          if (lane == 0) o = atomicAdd(&L.sv[2], (uint32_t)__popcll((unsigned long long)m));
+          o = readlane_u32(o, 0) + lanes_below(m);
+          if (cand && o < kSelCap) L.sel[o] = sel_order(f2key(key2f(k) / T), i);
+        }
+      }
+    }
+    __syncthreads();
+    c = L.sv[2];  // >= K: every raw key at or above t is a candidate
+  }
+  if (tlo != 0u && c <= kSelCap) {
+    bitonic_sort_desc(L.sel, c);  // the first K are the row's top K
+    return;
+  }
+  for (uint32_t i = tid; i < V; i += kBlock) keys[i] = f2key(key2f(keys[i]) / T);
+  __syncthreads();
+  select_top(keys, V, K, L);
+}
+
 // ---------------------------------------------------------------------------
 // General path: one row, 1024 threads, scratch in HBM.
 // Scratch per row (Vp = V rounded up to 1024): keysA | cnt | idsA | keysB |
@@ -224,9 +275,11 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
           bv = v;
           bi = i;
         }
+      } else if (sel) {
+        keysA[i] = f2key(v);  // divided later, and only where it decides (select_top_raw)
       } else {
         keysA[i] = f2key(v / T);
-        if (!sel) idsA[i] = i;
+        idsA[i] = i;
       }
     }
   }
@@ -240,7 +293,7 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   }
   __syncthreads();
   if (sel) {
-    select_top(keysA, V, n, L);
+    select_top_raw(keysA, V, n, T, L);
     if (wave == 0) {
       draw_tail_lds(a, b, len_b, P, n, [&](uint32_t i) { return (uint32_t)(L.sel[i] >> 32); },
                     [&](uint32_t i) { return ~(uint32_t)L.sel[i]; }, a.rng_state[b], L.exptab,
