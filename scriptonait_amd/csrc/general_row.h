@@ -136,20 +136,33 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
 
 // select_top for keys taken before the division by T (keys[i] = f2key(v_i)):
 // division is monotone, so every value of the top K after it (ties by id)
-// lies at or above tlo, the lowest raw key whose quotient equals that of the
-// K-th largest raw key, and only those values are divided. When tlo is not
-// bounded (a tie run longer than 64 keys, or a K-th value at -inf or NaN)
-// or the candidates outnumber the list, every key is divided in place and
-// select_top runs on them.
+// lies at or above tlo, the lowest raw key whose quotient equals that of
+// any raw key t0 at or below the K-th largest, and only those values are
+// divided and sorted. When tlo is not bounded (a tie run longer than 64
+// keys, or a t0 at -inf or NaN) or the candidates outnumber the list, every
+// key is divided in place and select_top runs on them.
 __device__ __forceinline__ void select_top_raw(uint32_t* keys, uint32_t V, uint32_t K, float T, GenLds& L) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  uint32_t t, r;
-  select_kth(keys, V, K, L, t, r);
-  const uint32_t tlo = lower_past_ties(t, T, lane);  // the same in every wave
-  uint32_t c = 0u;
-  if (tlo != 0u) {
-    if (tid == 0) L.sv[2] = 0u;
+  // t0: for K <= kSelCap / 2, the lower edge of the fine bin holding the
+  // K-th largest group maximum (L.wc, counted by the keys pass), so at
+  // least K values lie at or above it and t0 is at or below the K-th largest
+  // raw key (about 1.1-1.3 K values are listed); for a larger K, whose group
+  // bound would list more than the list holds, the K-th largest raw key
+  // itself, by the radix select.
+  uint32_t t0;
+  if (K <= kSelCap / 2u) {
+    coarse_from_fine(L.wc, L.bins);
     __syncthreads();
+    t0 = hist_locate(L.bins, L.wc, K, lane).lo;  // the same in every wave
+  } else {
+    uint32_t r;
+    select_kth(keys, V, K, L, t0, r);
+  }
+  const uint32_t tlo = t0 ? lower_past_ties(t0, T, lane) : 0u;
+  uint32_t c = 0u;
+  if (tid == 0) L.sv[2] = 0u;
+  __syncthreads();  // every wave is past the histogram, which the fallback's select reuses
+  if (tlo != 0u) {
     // Coalesced, as in select_top: wave w walks ids [w*R, (w+1)*R).
     const uint32_t R = ((V + kWaves - 1u) / kWaves + 63u) & ~63u;
     const uint32_t w0 = wave * R, w1 = min(V, w0 + R);
@@ -174,7 +187,7 @@ __device__ __forceinline__ void select_top_raw(uint32_t* keys, uint32_t V, uint3
       }
     }
     __syncthreads();
-    c = L.sv[2];  // >= K: every raw key at or above t is a candidate
+    c = L.sv[2];  // >= K: every value at or above t0 is a candidate
   }
   if (tlo != 0u && c <= kSelCap) {
     bitonic_sort_desc(L.sel, c);  // the first K are the row's top K
@@ -249,6 +262,12 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   const float T = P.temperature, rp = P.repetition_penalty;
   const uint32_t n = (P.top_k > 0 && P.top_k < V) ? P.top_k : V;
   const bool sel = n < V && n <= kSelCap;  // a top-k row whose K fits the LDS list
+  if (sel) {
+    // Fine histogram (key bits 31..20) of the maxima of the groups of 8
+    // values a thread takes at a time, for the select's bound.
+    reinterpret_cast<uint4*>(L.wc)[tid] = make_uint4(0u, 0u, 0u, 0u);  // kWaves * 256 == 4 * kBlock
+    __syncthreads();
+  }
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
   // Eight elements per thread in flight: their loads go out before any use.
@@ -263,6 +282,7 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
       mc[u] = (use_pen && i < V) ? __hip_atomic_load(&cnt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
       mo[u] = i < V && masked_out(a, i);
     }
+    float gm = -INFINITY;  // the group's largest value (NaN never is)
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
       const uint32_t i = i0 + u * kBlock;
@@ -277,11 +297,13 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
         }
       } else if (sel) {
         keysA[i] = f2key(v);  // divided later, and only where it decides (select_top_raw)
+        gm = fmaxf(gm, v);
       } else {
         keysA[i] = f2key(v / T);
         idsA[i] = i;
       }
     }
+    if (sel && gm > -INFINITY) atomicAdd(&L.wc[f2key(gm) >> 20], 1u);
   }
   if (greedy) {
     const uint32_t w = block_argmax(bv, bi, L.redv, L.redi);
