@@ -55,7 +55,8 @@ def test_hand_over_rows_penalty_below_one(sampler, k):
     compare(g, o, f"rp<1 k={k}")
 
 
-@pytest.mark.parametrize("V,k", [(4097, 4096), (5000, 4999), (40000, 3000), (131072, 4000)])
+@pytest.mark.parametrize("V,k", [(4097, 4096), (5000, 4999), (40000, 3000), (131072, 4000), (50257, 50),
+                                 (40000, 2048), (131072, 64)])
 def test_top_k_select_other_vocab_sizes(sampler, V, k):
     w = make_workload(3, B=4, V=V)
     prm = make_params(1.0, k, 0.98, 0.01, 1.1)
