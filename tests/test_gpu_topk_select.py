@@ -35,6 +35,24 @@ def test_top_k_select_with_ties_at_the_cut(sampler, V, k):
     compare(g, o, f"quantized V={V} k={k}")
 
 
+@pytest.mark.parametrize("case", ["long_tie_runs", "crowded_bound"])
+def test_sorting_path_select_fallbacks(sampler, case):
+    """V = 40000 top-k rows whose bound cannot be used as is: T = 100 makes
+    division merge runs of about 200 adjacent keys (longer than the tie
+    lowering covers), and logits on a grid of step 6 put thousands of ids on
+    the value at the bound (more candidates than the list holds). Both
+    divide every key and select exactly; ids, kept counts, probabilities and
+    RNG states match the oracle."""
+    w = make_workload(3, B=16, V=40000)
+    if case == "long_tie_runs":
+        prm = make_params(100.0, 50, 0.9, 0.0, 1.0)
+    else:
+        w.logits[:] = np.round(w.logits / 6.0) * 6.0
+        prm = make_params(1.0, 2000, 0.95, 0.0, 1.0)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, case)
+
+
 def test_top_k_select_fewer_allowed_than_k(sampler):
     """Only 700 ids allowed and K = 2000: the cut falls among the -inf keys."""
     w = make_workload(3, B=8)
