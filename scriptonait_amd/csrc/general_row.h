@@ -140,8 +140,11 @@ __device__ __forceinline__ void select_top(const uint32_t* keys, uint32_t V, uin
 // any raw key t0 at or below the K-th largest, and only those values are
 // divided and sorted. When tlo is not bounded (a tie run longer than 64
 // keys, or a t0 at -inf or NaN) or the candidates outnumber the list, every
-// key is divided in place and select_top runs on them.
-__device__ __forceinline__ void select_top_raw(uint32_t* keys, uint32_t V, uint32_t K, float T, GenLds& L) {
+// key is divided in place and select_top runs on them. Returns the sorted
+// list: L.sel, or L.wc's words read as order keys when the listed values
+// (at most 2048) were merge-sorted with L.sel as the first buffer.
+__device__ __forceinline__ const uint64_t* select_top_raw(uint32_t* keys, uint32_t V, uint32_t K, float T,
+                                                          GenLds& L) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   // t0: for K <= kSelCap / 2, the lower edge of the fine bin holding the
   // K-th largest group maximum (L.wc, counted by the keys pass), so at
@@ -189,13 +192,19 @@ __device__ __forceinline__ void select_top_raw(uint32_t* keys, uint32_t V, uint3
     __syncthreads();
     c = L.sv[2];  // >= K: every value at or above t0 is a candidate
   }
+  // The first K of the sorted list are the row's top K.
   if (tlo != 0u && c <= kSelCap) {
-    bitonic_sort_desc(L.sel, c);  // the first K are the row's top K
-    return;
+    static_assert(sizeof(L.wc) >= 2u * kBlock * sizeof(uint64_t), "the merge's second buffer");
+    uint64_t* tmp = reinterpret_cast<uint64_t*>(L.wc);
+    if (c <= kBlock) return sort_desc_lds<1>(L.sel, tmp, c);
+    if (c <= 2u * kBlock) return sort_desc_lds<2>(L.sel, tmp, c);
+    bitonic_sort_desc(L.sel, c);
+    return L.sel;
   }
   for (uint32_t i = tid; i < V; i += kBlock) keys[i] = f2key(key2f(keys[i]) / T);
   __syncthreads();
   select_top(keys, V, K, L);
+  return L.sel;
 }
 
 // ---------------------------------------------------------------------------
@@ -315,11 +324,12 @@ __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, Gen
   }
   __syncthreads();
   if (sel) {
-    select_top_raw(keysA, V, n, T, L);
+    const uint64_t* srt = select_top_raw(keysA, V, n, T, L);
+    // The tail stages its terms in whichever buffer the sorted list is not in.
+    float* buf = srt == L.sel ? reinterpret_cast<float*>(L.wc) : reinterpret_cast<float*>(L.sel);
     if (wave == 0) {
-      draw_tail_lds(a, b, len_b, P, n, [&](uint32_t i) { return (uint32_t)(L.sel[i] >> 32); },
-                    [&](uint32_t i) { return ~(uint32_t)L.sel[i]; }, a.rng_state[b], L.exptab,
-                    reinterpret_cast<float*>(L.wc));
+      draw_tail_lds(a, b, len_b, P, n, [&](uint32_t i) { return (uint32_t)(srt[i] >> 32); },
+                    [&](uint32_t i) { return ~(uint32_t)srt[i]; }, a.rng_state[b], L.exptab, buf);
     }
     return;
   }
