@@ -16,7 +16,7 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   if (__builtin_expect(!fast_row<NCH, VEC, GREEDY, CMODE, BIGK>(a, L), 0)) {
     if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
     __syncthreads();
-    general_row<false>(a, blockIdx.x, L.gen, true);  // greedy or K <= 1024: no whole-row sort
+    general_row<false>(a, blockIdx.x, L.gen, true);  // greedy or K <= kMaxFastK: no whole-row sort
   }
 }
 

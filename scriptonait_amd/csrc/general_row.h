@@ -217,8 +217,9 @@ __device__ __forceinline__ const uint64_t* select_top_raw(uint32_t* keys, uint32
 // counts_moved: the row's count table (decode-step mode with counts) was
 // already moved to this step's window by the kernel that handed it over.
 // SORT = false leaves out the whole-row sort, for the register path's
-// hand-overs: those are greedy rows and top-k rows with K <= 1024, which
-// select in LDS (K <= kSelCap), and the kernel is 20 KB of code smaller.
+// hand-overs: those are greedy rows and top-k rows with K <= kMaxFastK,
+// which select in LDS (K <= kSelCap), and the kernel is 20 KB of code
+// smaller.
 template <bool SORT = true>
 __device__ __forceinline__ void general_row(const SampleArgs& a, uint32_t b, GenLds& L, bool counts_moved) {
   const llmhip_params P = load_params(a, b);
