@@ -900,12 +900,16 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
       }
       if (lane == 0u) atomicAdd(&L.misc[kSampled], wave_positions<NCH, NS>(wave, V));
       if (lds_signal(&L.misc[kSyncSample]) == kTauWaves - 1u) {
+        // Every other wave waits for this one-wave chain: it takes the
+        // issue slots of its SIMD first (wave priority, reset below).
+        __builtin_amdgcn_s_setprio(3);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         LLMHIP_MARK(3);
         const uint32_t tkey = K <= kSpecMaxK ? lower_past_ties(hist_select(L.coarse, L.fine, spec_q(), false, lane), T, lane) : 0u;
         // A bounded threshold key is above 0x007fffff (lower_past_ties), so
         // 1 is free to say "not bounded".
         (void)lds_publish(&L.misc[kTauState], tkey ? tkey : 1u);
+        __builtin_amdgcn_s_setprio(0);
       }
     }
   }
@@ -1025,6 +1029,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
   // for the ALUs).
   if (__builtin_expect(spec && n < K && !ovf, 0)) {
     if (wave == 0u) {
+      __builtin_amdgcn_s_setprio(3);  // as for the first threshold
       const uint64_t q = spec_q();
       // q sample positions stand for (kSpecNum/kSpecDen)*K values; the
       // values below the first threshold are assumed to survive the penalty
@@ -1034,6 +1039,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
       const uint64_t q2 = want < 8u * q ? want : 8u * q;
       const uint32_t tk2 = lower_past_ties(hist_select(L.coarse, L.fine, (uint32_t)q2, false, lane), T, lane);
       (void)lds_publish(&L.misc[kTau2], tk2 != 0u && key2f(tk2) < tf ? tk2 : 1u);
+      __builtin_amdgcn_s_setprio(0);
     }
     const uint32_t tk2 = lds_wait_nonzero(&L.misc[kTau2], 1u, a);
     const bool again = tk2 > 1u;
@@ -1104,12 +1110,14 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
     // A finite maximum's key is at least 0x00800000, above -inf's and NaN's
     // (hist_locate's 0 says fewer than K threads hold a known value).
     if (wave == 0u) {
+      __builtin_amdgcn_s_setprio(3);  // as for the first threshold
       const uint32_t t0 = hist_locate(L.coarse, L.fine, K, lane).lo;
       // A large K goes to the per-slot narrowing below, which needs only
       // some key at or below its K-th largest known value: t0, or, when
       // fewer than K chunks hold a known value, the lowest finite key.
       const uint32_t tk = huge ? (t0 ? t0 : 0x00800000u) : t0 ? lower_past_ties(t0, T, lane) : 0u;
       (void)lds_publish(&L.misc[kTau0], tk ? tk : 1u);
+      __builtin_amdgcn_s_setprio(0);
     }
     const uint32_t tk0 = lds_wait_nonzero(&L.misc[kTau0], 1u, a);
     if (tk0 <= 1u) return false;
