@@ -79,13 +79,13 @@ constexpr uint32_t kSortedK = 1024;               // K up to which the sorted to
 constexpr uint32_t kBigCand = 7168;               // K > kSortedK: candidates per row (the scan entries' LDS)
 
 // misc[] slots
-constexpr int kSyncSample = 0;  // waves whose sample is in the histogram
+constexpr int kSyncSample = 0;  // sample waves in the histogram (bits 20+) and the positions they hold
 constexpr int kSyncHist = 1;    // waves whose history ids are counted
 constexpr int kCandN = 2;       // candidates in ord[]
 constexpr int kOverflow = 3;    // some wave's region overflowed
 constexpr int kTauState = 4;    // 0: not yet, 1: row not bounded here, else the threshold key
 constexpr int kArrive = 6;   // waves whose row has landed, in arrival order
-constexpr int kSampled = 7;  // row positions held by the sample waves
+constexpr int kSampled = 7;  // row positions held by the sample waves (for a second pass)
 constexpr int kSyncZero = 8; // waves whose share of the count table is zeroed
 constexpr int kGreedyMax = 9; // greedy rows: key of the row's largest value known without a penalty
 constexpr int kCandN2 = 10;    // candidates of the second speculative pass
@@ -878,10 +878,9 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
 
   // The sample position the speculative threshold takes: the target
   // (kSpecNum/kSpecDen)*K scaled to the positions the sample holds.
-  auto spec_q = [&]() __attribute__((always_inline)) {
+  auto spec_q = [&](uint32_t sampled) __attribute__((always_inline)) {
     // In 32 bits: sampled <= kTauWaves * 2048 and K <= kMaxFastK.
     static_assert((uint64_t)kSpecNum * kMaxFastK * kTauWaves * 2048u + kSpecDen * kMaxFastV < (1ull << 32), "fits");
-    const uint32_t sampled = L.misc[kSampled];
     return (kSpecNum * K * sampled + kSpecDen * V - 1u) / (kSpecDen * V) + 2u;
   };
   // 2. The first kTauWaves waves to get here put their sample maxima in the
@@ -898,14 +897,25 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
         atomicAdd(&L.coarse[k >> 24], 1u);
         atomicAdd(&L.fine[k >> 20], 1u);
       }
-      if (lane == 0u) atomicAdd(&L.misc[kSampled], wave_positions<NCH, NS>(wave, V));
-      if (lds_signal(&L.misc[kSyncSample]) == kTauWaves - 1u) {
+      // kSyncSample counts the sample waves in bits 20 and up and the row
+      // positions they hold below (at most kTauWaves * 2048): the last
+      // wave's own atomic returns the sample's size.
+      const uint32_t pos = wave_positions<NCH, NS>(wave, V);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      uint32_t before = 0u;
+      if (lane == 0u)
+        before = __hip_atomic_fetch_add(&L.misc[kSyncSample], (1u << 20) + pos, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_WORKGROUP);
+      before = readlane_u32(before, 0);
+      if ((before >> 20) == kTauWaves - 1u) {
+        const uint32_t sampled = (before & 0xfffffu) + pos;
+        if (lane == 0u) L.misc[kSampled] = sampled;  // for a second pass
         // Every other wave waits for this one-wave chain: it takes the
         // issue slots of its SIMD first (wave priority, reset below).
         __builtin_amdgcn_s_setprio(3);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         LLMHIP_MARK(3);
-        const uint32_t tkey = K <= kSpecMaxK ? lower_past_ties(hist_select(L.coarse, L.fine, spec_q(), false, lane), T, lane) : 0u;
+        const uint32_t tkey = K <= kSpecMaxK ? lower_past_ties(hist_select(L.coarse, L.fine, spec_q(sampled), false, lane), T, lane) : 0u;
         // A bounded threshold key is above 0x007fffff (lower_past_ties), so
         // 1 is free to say "not bounded".
         (void)lds_publish(&L.misc[kTauState], tkey ? tkey : 1u);
@@ -1030,7 +1040,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
   if (__builtin_expect(spec && n < K && !ovf, 0)) {
     if (wave == 0u) {
       __builtin_amdgcn_s_setprio(3);  // as for the first threshold
-      const uint64_t q = spec_q();
+      const uint64_t q = spec_q(L.misc[kSampled]);
       // q sample positions stand for (kSpecNum/kSpecDen)*K values; the
       // values below the first threshold are assumed to survive the penalty
       // two times in three, so 3/2 * (5K/4 - n) more of them are wanted.
