@@ -99,6 +99,19 @@ def test_register_path_k_above_1024(sampler, k, filters):
     compare(g, o, f"k={k} filters={filters}")
 
 
+@pytest.mark.parametrize("V,k", [(12000, 3000), (8000, 2500), (12001, 2000), (16384, 4096)])
+def test_register_path_k_above_1024_other_vocab_sizes(sampler, V, k):
+    """1024 < K <= 4096 with four or two chunks per lane (V = 12000, 8000:
+    fewer chunk maxima than K, so every known value is counted), an
+    unaligned row (V = 12001: scalar loads), and K = 4096 at V = 16384.
+    Rows the register path cannot bound may be handed over; every row must
+    match the oracle."""
+    w = make_workload(3, B=16, V=V)
+    prm = make_params(0.8, k, 0.95, 0.0, 1.15)
+    g, o = run_both(sampler, w, params=prm)
+    compare(g, o, f"V={V} k={k}")
+
+
 @pytest.mark.parametrize("k", [350, 512, 2000])
 def test_register_path_retries_with_a_mask_and_penalty(sampler, k):
     """K = 350 / 512 take the proven threshold (the speculative one is not
