@@ -196,6 +196,15 @@ def test_decode_loop_greedy_drawing_its_own_top_ids(sampler):
          max_prompt=50, fixed=0.3, counts=True, eos_rows=4)
 
 
+@pytest.mark.parametrize("counts", [False, True])
+def test_decode_loop_sorting_path_top_k(sampler, counts):
+    """V = 40000 top-k rows (beyond the register path's V): the sorting
+    path's select bound, list and merge sort inside a decode loop, with the
+    ring's window as the history (and the count table kept current)."""
+    _run(sampler, 40000, make_params(0.7, 50, 0.95, 0.05, 1.15), steps=12, B=8, window=256, cap=320,
+         max_prompt=200, counts=counts)
+
+
 def test_decode_loop_with_count_table_and_cache_resets(sampler):
     """hist_start jumps at each cache reset: the table is rebuilt there and
     slid between resets."""
