@@ -25,7 +25,8 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libllmhip_sampler.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["sampler_kernels.hip", "fast_counts.hip", "tied_head.hip", "sampler_api.hip", "scck_reader.cpp"]
+SOURCES = ["sampler_kernels.hip", "fast_nch8.hip", "fast_nch_small.hip", "fast_counts.hip", "fast_counts8.hip",
+           "fast_counts_small.hip", "tied_head.hip", "sampler_api.hip", "scck_reader.cpp"]
 ARCH = "gfx950"
 
 
@@ -79,8 +80,9 @@ def build_library(verbose: bool = False) -> Path:
     if verbose:
         for cmd in cmds:
             print(" ".join(cmd), flush=True)
-    # The sources compile independently; the two kernel files dominate.
-    with ThreadPoolExecutor(max_workers=min(len(cmds), 4)) as pool:
+    # The sources compile independently; the kernel files dominate.
+    workers = max(1, min(len(cmds), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
         for r in list(pool.map(lambda c: subprocess.run(c, check=True), cmds)):
             pass
     tmp = LIB_PATH.with_suffix(".so.tmp")

@@ -51,6 +51,18 @@ hipError_t launch_fast_nch(const SampleArgs& a0, bool vec, bool bigk, hipStream_
   return hipGetLastError();
 }
 
+// Each (NCH, CMODE) instantiation is compiled in a file of its own
+// (fast_nch8.hip, fast_nch_small.hip, fast_counts8.hip,
+// fast_counts_small.hip), so the library's kernels build in parallel.
+extern template hipError_t launch_fast_nch<1, false>(const SampleArgs&, bool, bool, hipStream_t);
+extern template hipError_t launch_fast_nch<2, false>(const SampleArgs&, bool, bool, hipStream_t);
+extern template hipError_t launch_fast_nch<4, false>(const SampleArgs&, bool, bool, hipStream_t);
+extern template hipError_t launch_fast_nch<8, false>(const SampleArgs&, bool, bool, hipStream_t);
+extern template hipError_t launch_fast_nch<1, true>(const SampleArgs&, bool, bool, hipStream_t);
+extern template hipError_t launch_fast_nch<2, true>(const SampleArgs&, bool, bool, hipStream_t);
+extern template hipError_t launch_fast_nch<4, true>(const SampleArgs&, bool, bool, hipStream_t);
+extern template hipError_t launch_fast_nch<8, true>(const SampleArgs&, bool, bool, hipStream_t);
+
 template <bool CMODE>
 hipError_t launch_fast_mode(const SampleArgs& a, bool vec, bool bigk, hipStream_t s) {
   switch (fast_nch(a.V)) {

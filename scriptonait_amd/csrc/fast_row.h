@@ -159,6 +159,18 @@ __device__ __forceinline__ float apply_penalty(float v, uint32_t m, float rp) {
   return v;
 }
 
+// The same, for a caller that only asks whether the result reaches `floor`
+// (and uses the value only when it does): with rp >= 1 every step can only
+// lower the value (v / rp <= v for v > 0, v * rp <= v otherwise, each
+// correctly rounded) or turn it into NaN, so once it is below floor the
+// result is below floor (or NaN) whatever the remaining steps do, and the
+// loop stops there. A history that repeats a top candidate's id many times
+// otherwise runs one dependent division per occurrence.
+__device__ __forceinline__ float apply_penalty_above(float v, uint32_t m, float rp, float floor) {
+  for (; m && !(v < floor); --m) v = v > 0.0f ? v / rp : v * rp;
+  return v;
+}
+
 __device__ __forceinline__ bool masked_out(const SampleArgs& a, uint32_t id) {
   // generate.rs:333-341
   if (id >= a.allowed_len || id == a.eos_id) return false;
@@ -754,17 +766,19 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
     lds_signal(&L.misc[kSyncHist]);
   };
   // Mask and penalty of this thread's slot e, in the reference's order.
-  auto fix_value = [&](float v, int e, uint32_t pmv) __attribute__((always_inline)) {
+  // floor: a value that falls below it can no longer matter (-inf: none).
+  auto fix_value = [&](float v, int e, uint32_t pmv, float floor) __attribute__((always_inline)) {
     if ((mkbits >> e) & 1u) v = -INFINITY;
-    if ((pmv >> e) & 1u) v = apply_penalty(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3)), rp);
+    if ((pmv >> e) & 1u)
+      v = apply_penalty_above(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (e & 3)), rp, floor);
     return v;
   };
-  auto fix_all = [&](uint32_t pmv) __attribute__((always_inline)) {
+  auto fix_all = [&](uint32_t pmv, float floor) __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       if ((((pmv | mkbits) >> (4 * c)) & 0xfu) != 0u) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[4 * c + j] = fix_value(x[4 * c + j], 4 * c + j, pmv);
+        for (int j = 0; j < 4; ++j) x[4 * c + j] = fix_value(x[4 * c + j], 4 * c + j, pmv, floor);
       }
     }
   };
@@ -840,9 +854,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
 #pragma unroll
       for (int e = 0; e < NCH * 4; ++e)
         if (x[e] >= m0) need |= 1u << e;
-      fix_all(pmv & need);
+      // A value pushed below M0 loses too, so its penalty stops there.
+      fix_all(pmv & need, m0);
     } else {
-      fix_all(pmv);
+      fix_all(pmv, -INFINITY);  // rp < 1 raises values: every step counts
     }
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
@@ -1006,7 +1021,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
         const uint32_t e = 4u * c + j, pos = base + j;
         if (ok) {
           if ((mkown >> e) & 1u) v = -INFINITY;
-          if ((pmown >> e) & 1u) v = apply_penalty(v, count_of(pos), rp);
+          if ((pmown >> e) & 1u) v = apply_penalty_above(v, count_of(pos), rp, tf);
           ok = v >= tf;
         }
         const uint64_t mk = __ballot(ok);
@@ -1207,7 +1222,8 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
         float v = x[e];
         bool ok = v >= tf && ((mkbits >> e) & 1u) == 0u;
         if (ok && ((pmr >> e) & 1u)) {
-          v = apply_penalty(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3)), rp);
+          v = apply_penalty_above(v, count_of(chunk_pos<NCH>((uint32_t)(e >> 2), wave, lane) + (uint32_t)(e & 3)), rp,
+                                  tf);
           ok = v >= tf;
         }
         x[e] = v;
