@@ -47,6 +47,9 @@ def parse_args():
     ap.add_argument("--tied-head", type=int, default=0, metavar="H",
                     help="time llmhip_sample_tied_head_device (logits = hidden[B,H] @ embed[V,H]^T, then the "
                          "sampler) on the workload's shape instead of the headline line")
+    ap.add_argument("--mixed", action="store_true",
+                    help="time one call whose rows mix four classes (greedy, top-k, whole vocabulary, "
+                         "top-k above the register path) against the sum of one call per class")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -166,6 +169,77 @@ def bench_tied_head(args) -> None:
     sampler.close()
 
 
+# Row classes of the --mixed line: (temperature, top_k, top_p, min_p,
+# repetition_penalty); top_k None keeps the workload's own.
+MIXED_KINDS = [("greedy", (0.0, None, 0.9, 0.1, 1.2)), ("top-k", (1.0, None, 0.9, 0.1, 1.2)),
+               ("whole vocabulary", (1.0, 0, 0.9, 0.1, 1.2)), ("top-k 5000", (1.0, 5000, 0.9, 0.1, 1.2))]
+
+
+def bench_mixed(args) -> None:
+    """One call over B rows of four classes in turn (row b has class b % 4)
+    against four calls of B/4 rows, one per class, on the same rows. Each
+    launch of the mixed call skips the rows of the other classes before
+    reading them, so the mixed call should cost no more than the sum."""
+    import torch
+
+    from scriptonait_amd.sampler import Sampler
+    from scriptonait_amd.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload(args.config, B=args.batch)
+    B = w.B - w.B % len(MIXED_KINDS)
+    prm = np.repeat(w.params, B)
+    for i, (_, (t, k, p, mp, rp)) in enumerate(MIXED_KINDS):
+        sel = np.arange(B) % len(MIXED_KINDS) == i
+        prm["temperature"][sel], prm["top_p"][sel], prm["min_p"][sel] = t, p, mp
+        prm["repetition_penalty"][sel] = rp
+        if k is not None:
+            prm["top_k"][sel] = k
+    sampler = Sampler(0)
+    stream = torch.cuda.current_stream(dev)
+    base = torch.from_numpy(w.logits[:B]).to(dev)
+    set_bytes = B * w.ld * 4
+    n_sets = max(2, int(np.ceil(2 * MALL_BYTES / set_bytes)) + 1)
+    sets = [torch.roll(base, shifts=s, dims=0).contiguous() for s in range(n_sets)]
+    rng = torch.from_numpy(w.rng_seeds[:B].view(np.int64).copy()).to(dev)
+    ids = torch.empty(B, dtype=torch.int32, device=dev)
+    per_class = []  # (name, row indices, params, logits sets, rng, ids)
+    for i, (name, _) in enumerate(MIXED_KINDS):
+        idx = np.nonzero(np.arange(B) % len(MIXED_KINDS) == i)[0]
+        ti = torch.from_numpy(idx).to(dev)
+        per_class.append((name, prm[idx].copy(), [lg.index_select(0, ti).contiguous() for lg in sets],
+                          rng[ti].clone(), torch.empty(idx.size, dtype=torch.int32, device=dev)))
+
+    def timed(fn):
+        for i in range(args.warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps * 1e3
+
+    steps = max(1, min(args.steps, 1000))
+    mixed_us = timed(lambda i: sampler.sample_device(sets[i % n_sets], prm, rng, ids, V=w.V, stream=stream))
+    classes = {}
+    for name, cp, csets, crng, cids in per_class:
+        classes[name] = timed(lambda i, cp=cp, csets=csets, crng=crng, cids=cids: sampler.sample_device(
+            csets[i % n_sets], cp, crng, cids, V=w.V, stream=stream))
+    total = sum(classes.values())
+    print(json.dumps({
+        "metric": "mixed-class call vs one call per class, us per step",
+        "value": mixed_us, "unit": "us", "higher_is_better": False, "steps": steps, "warmup": args.warmup,
+        "config": {"workload": f"{w.name} rows, class b % 4 of: " + ", ".join(n for n, _ in MIXED_KINDS),
+                   "B": B, "V": w.V},
+        "per_class_us": classes, "sum_of_classes_us": total, "mixed_over_sum": mixed_us / total,
+        "dtype": "f32", "data": f"synthetic ({w.name}, {n_sets} rotating device input sets)",
+    }), flush=True)
+    sampler.close()
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -180,6 +254,9 @@ def main():
         return
     if args.tied_head:
         bench_tied_head(args)
+        return
+    if args.mixed:
+        bench_mixed(args)
         return
 
     import torch

@@ -139,10 +139,10 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
                          uint32_t* out_kept, void* stream);
 
 /*
- * llmhip_sample_device for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). No counterpart in the reference: its sampler allocates a Vec
- * per call (generate.rs:331, :364). Same arguments, meaning and results as
+ * llmhip_sample_device for callers that cannot allocate device memory
+ * (tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference: its sampler allocates a Vec per call (generate.rs:331,
+ * :364). Same arguments, meaning and results as
  * llmhip_sample_device; the difference is where the device memory comes
  * from. This call allocates nothing: the per-row parameters (params_stride
  * != 0), the allowed mask's slot layout and the sorting path's per-row
@@ -160,6 +160,10 @@ int llmhip_sample_device(llmhip_ctx* ctx, const float* logits, size_t B, size_t 
  * threads) race and must be serialized by the caller. The kernels write
  * every scratch word they read within the call, so the array's contents
  * from an earlier call do not matter.
+ * The call is not meant for recording into a HIP graph: it reads params on
+ * the host to choose the kernels (a replay would keep the choice made at
+ * capture), copies per-row params from the caller's host memory with
+ * hipMemcpyAsync, and clears out_probs (when given) with hipMemsetAsync.
  */
 #define LLMHIP_NOALLOC_SCRATCH_BYTES (96u << 20)
 int llmhip_sample_device_noalloc(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
@@ -211,7 +215,11 @@ int llmhip_sample_tied_head_device(llmhip_ctx* ctx, const float* hidden, size_t 
  *
  *   ring      device [B][ring_cap] u32: row b's token history (prompt and
  *             generated tokens) as a ring; the caller fills it with the
- *             prompt and sets ring_len
+ *             prompt and sets ring_len. The prompt is what Generator::new
+ *             prefills (generate.rs:131-139): an empty prompt is [BOS], and
+ *             a prompt longer than context_len keeps only its last
+ *             context_len tokens; the caller applies both rules before it
+ *             fills the ring, so that step 1's `recent` is the reference's
  *   ring_len  device [B] u32 in/out: tokens row b has seen so far
  *   done      device nullable [B] u32 in/out
  *   hist_start device nullable [B] u32: the first token (counted from the
@@ -310,7 +318,9 @@ int llmhip_decode_step_bits(llmhip_ctx* ctx, const float* logits, size_t B, size
  * wait between wavefronts that ran out of spins; a bug, never an input
  * condition) records it in a device word instead. This call waits for
  * `stream`, reads the words that the device entries' kernels set since the
- * last call, and clears them. llmhip_sample_host keeps a word of its own,
+ * last call, and clears them, each in one atomic exchange on the device (a
+ * flag that a kernel on another stream sets meanwhile is reported now or by
+ * the next call, never lost). llmhip_sample_host keeps a word of its own,
  * cleared at its start, and reports its own kernels' flags as its return
  * status.
  *   flags      LLMHIP_KSTATUS_* bits of device-entry calls (0: all well; the

@@ -584,7 +584,10 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
                "s"(a.done), "s"(a.ring_cap), "s"(a.window), "s"(a.hist_start), "s"(a.spin_limit));
   asm volatile("" ::"s"(a.shared.temperature), "s"(a.shared.top_k), "s"(a.shared.top_p), "s"(a.shared.min_p),
                "s"(a.shared.repetition_penalty), "s"(a.eos_id), "s"(a.allowed), "s"(a.allowed_len), "s"(a.B),
-               "s"(a.scratch), "s"(a.scratch_row_words));
+               "s"(a.scratch), "s"(a.scratch_row_words), "s"(a.row_cls_on));
+  // A row of another class than this launch's (a mixed call): nothing to do,
+  // and nothing is read for it.
+  if (!row_in_launch(a, b)) return true;
   LLMHIP_MARK(0);
 
   // Every global load below is issued unconditionally (positions past V and

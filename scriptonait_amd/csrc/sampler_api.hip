@@ -30,6 +30,7 @@ hipError_t launch_general(const SampleArgs& a, hipStream_t s);
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s);
+hipError_t launch_take_status(uint32_t* words, hipStream_t s);
 hipError_t launch_tied_head(const float* hidden, uint64_t ldh, const float* embed, uint64_t lde, float* logits,
                             uint64_t ldl, uint32_t B, uint32_t V, uint32_t h, hipStream_t s);
 }  // namespace llmhip
@@ -223,11 +224,13 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   }
   uint32_t classes = 0;
   bool bigk = false;  // some top-k row of the register path has K > 64
+  uint32_t row_cls[128] = {};  // each row's class index (SampleArgs::row_cls), for calls of <= kRowClsRows rows
   for (size_t b = 0; b < (params_stride ? B : 1); ++b) {
     const llmhip_params& p = params_host[b * params_stride];
     const uint32_t c = row_class(p, (uint32_t)V);
     classes |= c;
     bigk = bigk || (c == kClassTopK && p.top_k > 64u);
+    if (b < kRowClsRows) row_cls[b >> 4] |= (uint32_t)__builtin_ctz(c) << ((b & 15u) * 2u);
   }
   const bool fast_ok = V <= kMaxFastV;
   const uint32_t fast_mask = fast_ok ? (classes & (kClassGreedy | kClassTopK)) : 0u;
@@ -281,6 +284,12 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.spin_limit = ctx->spin_limit;
   a.scratch = scr;
   a.scratch_row_words = row_words;
+  // Rows of several classes: one launch per class, and each launch's
+  // workgroups skip the rows of the others before reading them.
+  if (params_stride && B <= kRowClsRows && __builtin_popcount(classes) > 1) {
+    a.row_cls_on = 1u;
+    memcpy(a.row_cls, row_cls, sizeof row_cls);
+  }
 
   if (out_probs) HIP_TRY(hipMemsetAsync(out_probs, 0, B * V * sizeof(float), s));
   // 128-bit row loads need 16-byte aligned rows and V % 4 == 0 (a row's
@@ -711,15 +720,15 @@ int llmhip_ctx_status(llmhip_ctx* ctx, void* stream, llmhip_status* out) {
   Device d(ctx->device);
   if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  uint32_t w[kStatusWords] = {0u, 0u, 0u, 0u};
-  HIP_TRY(hipMemcpyAsync(w, ctx->status.ptr, sizeof w, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipStreamSynchronize(s));
-  // The host entry's word stays: it is cleared by each host call itself.
+  // Read and clear in one step on the device (atomic exchanges), then copy
+  // what was taken. The host entry's word stays: each host call clears it.
   uint32_t* dev = static_cast<uint32_t*>(ctx->status.ptr);
-  HIP_TRY(hipMemsetAsync(dev + kStatusDeviceWord, 0, 2 * sizeof(uint32_t), s));
+  uint32_t w[2] = {0u, 0u};
+  HIP_TRY(launch_take_status(dev, s));
+  HIP_TRY(hipMemcpyAsync(w, dev + kStatusTakenWord, sizeof w, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
-  out->flags = w[kStatusDeviceWord];
-  out->handovers = w[kStatusHandoverWord];
+  out->flags = w[0];
+  out->handovers = w[1];
   return LLMHIP_OK;
 }
 

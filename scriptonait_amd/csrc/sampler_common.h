@@ -102,7 +102,25 @@ struct SampleArgs {
   uint32_t* scratch;   // general path: per-row words
   uint64_t scratch_row_words;
   uint32_t row_class_mask;  // which row classes this launch handles
+  // Each row's class (log2 of its RowClass bit, two bits per row: row b in
+  // bits 2(b % 16) of word b / 16), when row_cls_on: a call whose rows fall
+  // into several classes runs one launch per class, and each launch's
+  // workgroups return before reading anything for a row of another class.
+  // Filled by the host (which reads the parameters anyway) for calls of at
+  // most kRowClsRows rows; otherwise a row's class comes from its
+  // parameters, after the loads the register path issues first.
+  uint32_t row_cls_on;
+  uint32_t row_cls[128];
 };
+constexpr uint32_t kRowClsRows = 16u * 128u;
+
+// Whether row b belongs to this launch, from the host-made class table
+// (true when the table is off).
+__device__ __forceinline__ bool row_in_launch(const SampleArgs& a, uint32_t b) {
+  if (!a.row_cls_on) return true;
+  const uint32_t c = (a.row_cls[b >> 4] >> ((b & 15u) * 2u)) & 3u;
+  return ((1u << c) & a.row_class_mask) != 0u;
+}
 
 // Row b's history (`recent`, generate.rs:343-352): the CSR slice
 // hist[hist_offsets[b] .. hist_offsets[b+1]), or in decode-step mode the
@@ -285,7 +303,8 @@ constexpr uint32_t kSpinLimit = 1u << 20;    // default spins of a wait between 
 constexpr uint32_t kStatusHostWord = 0;      // flags of the current host-entry call
 constexpr uint32_t kStatusDeviceWord = 1;    // flags of device-entry calls since the last llmhip_ctx_status
 constexpr uint32_t kStatusHandoverWord = 2;  // rows handed to the sorting path since the last llmhip_ctx_status
-constexpr uint32_t kStatusWords = 4;
+constexpr uint32_t kStatusTakenWord = 4;     // where llmhip_ctx_status's kernel moves the device and hand-over words
+constexpr uint32_t kStatusWords = 6;
 
 constexpr uint32_t kBlock = 1024;
 constexpr uint32_t kWaves = kBlock / 64;

@@ -1,17 +1,22 @@
 // gfx950 kernels of the decode-time sampler.
 //
 // One 1024-thread workgroup (16 wave64s) samples one row, so a batch of B
-// rows is B workgroups and B=256 fills the 256 CUs of an MI355X once. Two
+// rows is B workgroups and B=256 fills the 256 CUs of an MI355X once. Three
 // kernels share the row semantics of crates/llm-core/src/generate.rs:325-420:
 //
-//  * sample_fast_kernel (V <= 32768, 0 < top_k <= 1024, and greedy rows):
+//  * sample_fast_kernel (V <= 32768, 0 < top_k <= 4096, and greedy rows):
 //    the row stays in registers and the sample is decided while it streams
-//    in (fast_row.h).
+//    in (fast_row.h; its instantiations are compiled in fast_nch8.hip,
+//    fast_nch_small.hip, fast_counts8.hip and fast_counts_small.hip).
 //
-//  * sample_general_kernel (everything else: top_k == 0, top_k >= V, large
-//    V, and rows the fast kernel cannot bound): a stable LSD radix sort of
-//    (key, id) pairs in per-row HBM scratch gives exactly the reference's
-//    `order`, followed by the same sequential tail.
+//  * sample_vocab_kernel (top_k == 0 or top_k >= V: the whole vocabulary
+//    is kept): the reference's three folds replayed exactly over value
+//    buckets, without sorting the row (vocab_row.h).
+//
+//  * sample_general_kernel (top-k rows the fast kernel does not take, V >
+//    32768 or top_k > 4096, and rows the other two hand over): an LDS select
+//    of the top K, or a stable LSD radix sort of (key, id) pairs in per-row
+//    HBM scratch, then the same sequential tail (general_row.h).
 #include <algorithm>
 
 #include "draw_tail.h"
@@ -28,7 +33,7 @@ __global__ __launch_bounds__(kBlock) void sample_general_kernel(SampleArgs a) {
   __shared__ GenLds L;
   const uint32_t b = blockIdx.x;
   if (b >= a.B) return;
-  if (!(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  if (a.row_cls_on ? !row_in_launch(a, b) : !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   general_row(a, b, L, false);
 }
 
@@ -43,7 +48,7 @@ __global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
   } L;
   const uint32_t b = blockIdx.x;
   if (b >= a.B) return;
-  if (!(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  if (a.row_cls_on ? !row_in_launch(a, b) : !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   const bool vec4 = (reinterpret_cast<uintptr_t>(a.logits) % 16u == 0u) && (a.ld % 4u == 0u);
   if (!vocab_row(a, b, L.v, vec4)) {
     if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
@@ -145,6 +150,22 @@ hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint
   const uint64_t per = words <= kSeenLdsWords ? 16u * kBlock : (uint64_t)kBlock;  // tokens per block and pass
   const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + per - 1u) / per, kSeenMaxBlocks);
   hipLaunchKernelGGL(seen_bits_kernel, dim3(blocks), dim3(kBlock), 0, s, tokens, n, V, bits);
+  return hipGetLastError();
+}
+
+// Moves the device-entry flags and the hand-over count to words[kStatusTakenWord ..
+// +1] and clears them, each in one atomic exchange: a kernel on another stream
+// that sets a flag or counts a hand-over meanwhile is either taken now or
+// left for the next call, never lost.
+__global__ void take_status_kernel(uint32_t* words) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    words[kStatusTakenWord] = atomicExch(&words[kStatusDeviceWord], 0u);
+    words[kStatusTakenWord + 1] = atomicExch(&words[kStatusHandoverWord], 0u);
+  }
+}
+
+hipError_t launch_take_status(uint32_t* words, hipStream_t s) {
+  hipLaunchKernelGGL(take_status_kernel, dim3(1), dim3(64), 0, s, words);
   return hipGetLastError();
 }
 

@@ -132,7 +132,9 @@ bool validate(const llmhip_scck_info& c, std::string& err) {
     err = buf;
     return false;
   }
-  if (!(c.rope_theta > 1.0f)) return small("rope_theta", 2);
+  // config.rs:209 tests `rope_theta <= 1.0`, which a NaN passes: such a
+  // file is accepted, as Checkpoint::from_bytes accepts it.
+  if (c.rope_theta <= 1.0f) return small("rope_theta", 2);
   const u128 training = param_count(c) * 4 * 4 + activation_bytes(c);  // config.rs:346-355
   if (training > kMaxTrainingBytes) {
     snprintf(buf, sizeof buf, "checkpoint config is invalid: needs more than %llu bytes to train",

@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 namespace llmhip {
 
 constexpr int kHeadRows = 32;     // rows per workgroup
@@ -37,13 +39,14 @@ struct HeadArgs {
   float* logits;        // [B][ldl]
   uint64_t ldh, lde, ldl;
   uint32_t B, V, h;
+  uint32_t row0;  // first row of this launch's grid.y tiles
 };
 
 __global__ __launch_bounds__(kHeadThreads) void tied_head_kernel(HeadArgs a) {
   __shared__ float4 xs[kHeadK / 4][kHeadRows];
   __shared__ float4 ws[kHeadK / 4][kHeadOuts];
   const uint32_t t = threadIdx.x, tr = t >> 5, to = t & 31u;
-  const uint32_t o0 = blockIdx.x * kHeadOuts, r0 = blockIdx.y * kHeadRows;
+  const uint32_t o0 = blockIdx.x * kHeadOuts, r0 = a.row0 + blockIdx.y * kHeadRows;
   const uint32_t h4 = a.h & ~3u;  // the four accumulators' part; the rest is the tail
 
   float acc[4][4][4];  // [row i][output i][accumulator k]
@@ -150,10 +153,19 @@ __global__ __launch_bounds__(kHeadThreads) void tied_head_kernel(HeadArgs a) {
 
 hipError_t launch_tied_head(const float* hidden, uint64_t ldh, const float* embed, uint64_t lde, float* logits,
                             uint64_t ldl, uint32_t B, uint32_t V, uint32_t h, hipStream_t s) {
-  HeadArgs a{hidden, embed, logits, ldh, lde, ldl, B, V, h};
-  dim3 grid((V + kHeadOuts - 1) / kHeadOuts, (B + kHeadRows - 1) / kHeadRows);
-  hipLaunchKernelGGL(tied_head_kernel, grid, dim3(kHeadThreads), 0, s, a);
-  return hipGetLastError();
+  HeadArgs a{hidden, embed, logits, ldh, lde, ldl, B, V, h, 0u};
+  // Row tiles go in grid.y, whose extent the device caps at 65535: a larger
+  // B takes several launches, each over the next rows.
+  constexpr uint32_t kMaxTilesY = 65535u;
+  const uint32_t tiles = (B + kHeadRows - 1) / kHeadRows;
+  for (uint32_t t0 = 0; t0 < tiles; t0 += kMaxTilesY) {
+    a.row0 = t0 * kHeadRows;
+    dim3 grid((V + kHeadOuts - 1) / kHeadOuts, std::min(kMaxTilesY, tiles - t0));
+    hipLaunchKernelGGL(tied_head_kernel, grid, dim3(kHeadThreads), 0, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace llmhip

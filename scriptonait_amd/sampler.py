@@ -23,6 +23,7 @@ import numpy as np
 from .workloads import PARAMS_DTYPE
 
 LIB_PATH = Path(__file__).resolve().parent / "libllmhip_sampler.so"
+BOS = 257  # crates/llm-core/src/tokenizer.rs:36
 EOS = 258  # crates/llm-core/src/tokenizer.rs:38
 
 LLMHIP_OK = 0
@@ -399,6 +400,23 @@ class Sampler:
 
 
 _default: Optional[Sampler] = None
+
+
+def prompt_ring_tokens(prompt: Sequence[int], context_len: int) -> np.ndarray:
+    """The tokens a decode-step ring starts with for `prompt`: what
+    Generator::new prefills (crates/llm-core/src/generate.rs:131-139). An
+    empty prompt becomes [BOS]; a prompt longer than context_len keeps only
+    its last context_len tokens. The ring's owner fills row b with these and
+    sets ring_len[b] to their count before the first llmhip_decode_step, so
+    that step 1's `recent` is the reference's."""
+    if context_len < 1:
+        raise ValueError("context_len must be at least 1")
+    tokens = np.asarray(prompt, dtype=np.uint32).reshape(-1)
+    if tokens.size == 0:
+        tokens = np.array([BOS], dtype=np.uint32)
+    if tokens.size > context_len:
+        tokens = tokens[tokens.size - context_len:]
+    return tokens.copy()
 
 
 def _default_sampler() -> Sampler:

@@ -164,3 +164,12 @@ def test_read_params_rejects_ranges_past_the_end():
     with pytest.raises(ValueError):
         c.params(w.size - 3, 4)
     assert c.params(w.size, 0).size == 0
+
+
+def test_accepts_a_nan_rope_theta_as_the_reference_does():
+    """config.rs:209 rejects `rope_theta <= 1.0`; NaN compares false there, so
+    Checkpoint::from_bytes accepts the file, and so does the reader."""
+    _, data = _sample(rope_theta=float("nan"))
+    got = Checkpoint.from_bytes(data)
+    assert np.isnan(got.config.rope_theta)
+    assert got.config.vocab_size == V

@@ -55,6 +55,24 @@ def test_per_row_mixed_params(sampler):
     compare(g, o, "mixed per-row params")
 
 
+@pytest.mark.parametrize("B", [2048, 2049])
+def test_mixed_classes_on_both_sides_of_the_host_class_table(sampler, B):
+    """A call of up to 2048 rows carries each row's class in the kernel
+    arguments (its launches skip other classes' rows before any load); a
+    larger one finds the class from the row's parameters. Both must sample
+    every row once, by the path of its own class."""
+    w = make_workload(2, B=B)
+    prm = np.zeros(B, dtype=PARAMS_DTYPE)
+    kinds = [(0.0, 50, 0.9, 0.1, 1.2), (1.0, 50, 0.9, 0.1, 1.2), (1.3, 0, 0.9, 0.0, 1.1),
+             (0.5, 5000, 0.5, 0.0, 1.0)]  # greedy, top-k, whole vocabulary, K above the register path
+    order = np.random.default_rng(B).integers(0, len(kinds), size=B)
+    for b in range(B):
+        prm[b] = kinds[order[b]]
+    g, o = run_both(sampler, w, params=prm, want_probs=False)
+    s = compare(g, o, f"mixed classes B={B}", probs=False)
+    assert s["mismatches"] == 0, s
+
+
 def test_allowed_mask(sampler):
     w = make_workload(2, B=16)
     allowed = np.ones(w.V - 100, dtype=np.uint8)  # ids past the mask stay allowed

@@ -57,3 +57,15 @@ def test_splitmix_stream_offsets():
 def test_config_table_matches_baseline():
     assert CONFIGS[3]["B"] == 256 and CONFIGS[3]["V"] == 32000 and CONFIGS[3]["k"] == 64
     assert CONFIGS[5]["V"] == 131072 and CONFIGS[5]["H"] == 2048
+
+
+def test_prompt_ring_tokens_follow_generator_new():
+    """generate.rs:131-139: an empty prompt is [BOS]; a long prompt keeps its
+    last context_len tokens; others are unchanged."""
+    from scriptonait_amd.sampler import BOS, prompt_ring_tokens
+
+    assert prompt_ring_tokens([], 8).tolist() == [BOS]
+    assert prompt_ring_tokens([5, 6, 7], 8).tolist() == [5, 6, 7]
+    assert prompt_ring_tokens(list(range(10)), 4).tolist() == [6, 7, 8, 9]
+    assert prompt_ring_tokens([], 1).tolist() == [BOS]
+    assert prompt_ring_tokens([1, 2], 2).tolist() == [1, 2]

@@ -3,11 +3,11 @@
 The no-alloc entry runs the same kernels as llmhip_sample_device, with its
 device memory (per-row parameters, the allowed mask's slot layout, the
 sorting path's per-row scratch) taken from the library's fixed per-GPU array
-instead of the context's buffers. Two calls in a row, the second smaller and
-of another kind, must give the same ids, RNG states, kept counts and
+instead of the context's buffers. Three calls in a row, each smaller than
+the last and of another kind, must give the same ids, RNG states, kept counts and
 probabilities as llmhip_sample_device on the same inputs: the array keeps the
-first call's contents, so the second shows that nothing depends on what an
-earlier call left there. A call larger than the array is refused with
+first call's contents, so the later ones show that nothing depends on what
+an earlier call left there. A call larger than the array is refused with
 LLMHIP_ERR_UNSUPPORTED before anything is enqueued.
 """
 import numpy as np
@@ -63,7 +63,7 @@ def test_noalloc_matches_the_allocating_entry_twice_in_a_row(sampler):
     w = make_workload(3)
     prm = np.repeat(w.params, w.B)
     prm["repetition_penalty"][np.arange(w.B) % 16 == 5] = 0.85  # handed to the sorting path (scratch)
-    prm["top_k"][np.arange(w.B) % 16 == 9] = 2000  # the sorting path's LDS select (scratch keys)
+    prm["top_k"][np.arange(w.B) % 16 == 9] = 2000  # the register path's large-K kernel (no scratch)
     sampler.status()
     first = _both_entries(sampler, w, prm)
     _same(*first)
@@ -86,6 +86,22 @@ def test_noalloc_matches_the_allocating_entry_twice_in_a_row(sampler):
                              want_probs=True)
     assert np.array_equal(second[1]["ids"], o2.ids)
     assert np.array_equal(second[1]["rng"], o2.rng_state)
+
+    print("no-alloc call 3: B=12, V=50257, top_k 40 and 1000 (the sorting path's select, keys in the array)",
+          flush=True)
+    w3 = make_workload(4, B=12)
+    prm3 = np.repeat(w3.params, w3.B)
+    prm3["top_k"] = np.where(np.arange(w3.B) % 2 == 0, 40, 1000)
+    prm3["repetition_penalty"] = 1.1
+    rs = np.random.default_rng(3)
+    w3.hist = rs.integers(0, w3.V, size=w3.B * 300).astype(np.uint32)
+    w3.hist_offsets = (np.arange(w3.B + 1) * 300).astype(np.uint32)
+    third = _both_entries(sampler, w3, prm3)
+    _same(*third)
+    assert sampler.status().flags == 0
+    o3 = oracle.sample_batch(w3.logits, prm3, w3.rng_seeds, w3.hist, w3.hist_offsets, V=w3.V)
+    assert np.array_equal(third[1]["ids"], o3.ids)
+    assert np.array_equal(third[1]["rng"], o3.rng_state)
 
 
 def test_noalloc_refuses_a_call_beyond_its_array(sampler):
