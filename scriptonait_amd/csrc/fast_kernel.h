@@ -16,7 +16,7 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
   if (__builtin_expect(!fast_row<NCH, VEC, GREEDY, CMODE, BIGK>(a, L), 0)) {
     if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
     __syncthreads();
-    general_row<false>(a, blockIdx.x, L.gen, true);  // greedy or K <= kMaxFastK: no whole-row sort
+    general_row<false>(a, launch_row(a), L.gen, true);  // greedy or K <= kMaxFastK: no whole-row sort
   }
 }
 
@@ -26,26 +26,27 @@ __global__ __launch_bounds__(kBlock) void sample_fast_kernel(SampleArgs a) {
 template <int NCH, bool CMODE>
 hipError_t launch_fast_nch(const SampleArgs& a0, bool vec, bool bigk, hipStream_t s) {
   SampleArgs a = a0;
-  if (a0.row_class_mask & kClassGreedy) {
-    a.row_class_mask = kClassGreedy;
+  uint32_t grid;
+  a.row_class_mask = kClassGreedy;
+  if ((a0.row_class_mask & kClassGreedy) && (grid = launch_grid(a)) != 0u) {
     if (vec) {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, true, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, true, CMODE, false>), dim3(grid), dim3(kBlock), 0, s, a);
     } else {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, true, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, true, CMODE, false>), dim3(grid), dim3(kBlock), 0, s, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (a0.row_class_mask & kClassTopK) {
-    a.row_class_mask = kClassTopK;
+  a.row_class_mask = kClassTopK;
+  if ((a0.row_class_mask & kClassTopK) && (grid = launch_grid(a)) != 0u) {
     if (vec && bigk) {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE, true>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE, true>), dim3(grid), dim3(kBlock), 0, s, a);
     } else if (vec) {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, true, false, CMODE, false>), dim3(grid), dim3(kBlock), 0, s, a);
     } else if (bigk) {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE, true>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE, true>), dim3(grid), dim3(kBlock), 0, s, a);
     } else {
-      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE, false>), dim3(a.B), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((sample_fast_kernel<NCH, false, false, CMODE, false>), dim3(grid), dim3(kBlock), 0, s, a);
     }
   }
   return hipGetLastError();

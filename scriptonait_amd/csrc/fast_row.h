@@ -570,8 +570,6 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
   static_assert(NCH * 4 <= 32, "slot masks are 32 bits");
   typedef float f4v __attribute__((ext_vector_type(4)));
 
-  // The grid is exactly B workgroups.
-  const uint32_t b = blockIdx.x;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
   const uint32_t V = a.V;
@@ -585,9 +583,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
   asm volatile("" ::"s"(a.shared.temperature), "s"(a.shared.top_k), "s"(a.shared.top_p), "s"(a.shared.min_p),
                "s"(a.shared.repetition_penalty), "s"(a.eos_id), "s"(a.allowed), "s"(a.allowed_len), "s"(a.B),
                "s"(a.scratch), "s"(a.scratch_row_words), "s"(a.row_cls_on));
-  // A row of another class than this launch's (a mixed call): nothing to do,
-  // and nothing is read for it.
-  if (!row_in_launch(a, b)) return true;
+  const uint32_t b = launch_row(a);
   LLMHIP_MARK(0);
 
   // Every global load below is issued unconditionally (positions past V and

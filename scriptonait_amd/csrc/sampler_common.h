@@ -6,6 +6,7 @@
 
 #include "../../include/llmhip_sampler.h"
 #include "glibc_expf.h"
+#include "wave_ops.h"
 
 namespace llmhip {
 
@@ -103,23 +104,59 @@ struct SampleArgs {
   uint64_t scratch_row_words;
   uint32_t row_class_mask;  // which row classes this launch handles
   // Each row's class (log2 of its RowClass bit, two bits per row: row b in
-  // bits 2(b % 16) of word b / 16), when row_cls_on: a call whose rows fall
-  // into several classes runs one launch per class, and each launch's
-  // workgroups return before reading anything for a row of another class.
+  // bits 2(b % 16) of word b / 16; zero past B), when row_cls_on. A call
+  // whose rows fall into several classes runs one launch per class (or
+  // group of classes); with the table, a launch's grid holds one workgroup
+  // per row of its classes (launch_row), so no workgroup is spent on the
+  // other rows and the working ones are consecutive, spread over all XCDs.
   // Filled by the host (which reads the parameters anyway) for calls of at
-  // most kRowClsRows rows; otherwise a row's class comes from its
-  // parameters, after the loads the register path issues first.
+  // most kRowClsRows rows; a larger mixed call runs B workgroups per launch
+  // and each finds its row's class from the row's parameters.
   uint32_t row_cls_on;
   uint32_t row_cls[128];
 };
 constexpr uint32_t kRowClsRows = 16u * 128u;
 
-// Whether row b belongs to this launch, from the host-made class table
-// (true when the table is off).
-__device__ __forceinline__ bool row_in_launch(const SampleArgs& a, uint32_t b) {
-  if (!a.row_cls_on) return true;
-  const uint32_t c = (a.row_cls[b >> 4] >> ((b & 15u) * 2u)) & 3u;
-  return ((1u << c) & a.row_class_mask) != 0u;
+// The row a workgroup samples: blockIdx.x, or, with the class table,
+// the blockIdx.x-th row (in row order) of the launch's classes. Every
+// thread of the workgroup calls it (full waves); lane l of each wave reads
+// table words 2l and 2l+1 (rows 32l .. 32l+31).
+__device__ __forceinline__ uint32_t launch_row(const SampleArgs& a) {
+  if (!a.row_cls_on) return blockIdx.x;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t w0 = a.row_cls[2u * lane], w1 = a.row_cls[2u * lane + 1u];
+  uint32_t m0 = 0u, m1 = 0u;  // bit 2i: field i holds one of the launch's classes
+#pragma unroll
+  for (uint32_t c = 0; c < 4u; ++c) {
+    if (!((a.row_class_mask >> c) & 1u)) continue;  // class index c is RowClass bit 1 << c
+    const uint32_t x0 = w0 ^ (c * 0x55555555u), x1 = w1 ^ (c * 0x55555555u);
+    m0 |= ~(x0 | (x0 >> 1)) & 0x55555555u;
+    m1 |= ~(x1 | (x1 >> 1)) & 0x55555555u;
+  }
+  const uint32_t n = (uint32_t)(__builtin_popcount(m0) + __builtin_popcount(m1));
+  const uint32_t incl = wave_incl_scan(n);
+  // The grid counts the launch's rows below B only, and the zero fields
+  // past B come after them in order, so the j-th match is a row below B.
+  const uint32_t j = blockIdx.x;
+  const uint32_t L = (uint32_t)__builtin_ctzll(__ballot(incl > j));
+  uint32_t r = j - (readlane_u32(incl, L) - readlane_u32(n, L));
+  uint32_t m = readlane_u32(m0, L), base = 32u * L;
+  const uint32_t n0 = (uint32_t)__builtin_popcount(m);
+  if (r >= n0) {
+    r -= n0;
+    m = readlane_u32(m1, L);
+    base += 16u;
+  }
+  for (; r; --r) m &= m - 1u;
+  return base + ((uint32_t)__builtin_ctz(m) >> 1);
+}
+
+// Workgroups of a launch over the classes in a.row_class_mask (host side).
+inline uint32_t launch_grid(const SampleArgs& a) {
+  if (!a.row_cls_on) return a.B;
+  uint32_t n = 0;
+  for (uint32_t b = 0; b < a.B; ++b) n += (a.row_class_mask >> ((a.row_cls[b >> 4] >> ((b & 15u) * 2u)) & 3u)) & 1u;
+  return n;
 }
 
 // Row b's history (`recent`, generate.rs:343-352): the CSR slice

@@ -31,9 +31,9 @@ namespace llmhip {
 
 __global__ __launch_bounds__(kBlock) void sample_general_kernel(SampleArgs a) {
   __shared__ GenLds L;
-  const uint32_t b = blockIdx.x;
+  const uint32_t b = launch_row(a);
   if (b >= a.B) return;
-  if (a.row_cls_on ? !row_in_launch(a, b) : !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  if (!a.row_cls_on && !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   general_row(a, b, L, false);
 }
 
@@ -46,9 +46,9 @@ __global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
     VocabLds v;
     GenLds gen;
   } L;
-  const uint32_t b = blockIdx.x;
+  const uint32_t b = launch_row(a);
   if (b >= a.B) return;
-  if (a.row_cls_on ? !row_in_launch(a, b) : !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  if (!a.row_cls_on && !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   const bool vec4 = (reinterpret_cast<uintptr_t>(a.logits) % 16u == 0u) && (a.ld % 4u == 0u);
   if (!vocab_row(a, b, L.v, vec4)) {
     if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
@@ -137,7 +137,9 @@ hipError_t launch_fast(const SampleArgs& a, bool vec, bool bigk, hipStream_t s) 
 }
 
 hipError_t launch_vocab(const SampleArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(sample_vocab_kernel, dim3(a.B), dim3(kBlock), 0, s, a);
+  const uint32_t grid = launch_grid(a);
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL(sample_vocab_kernel, dim3(grid), dim3(kBlock), 0, s, a);
   return hipGetLastError();
 }
 
@@ -170,7 +172,9 @@ hipError_t launch_take_status(uint32_t* words, hipStream_t s) {
 }
 
 hipError_t launch_general(const SampleArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(sample_general_kernel, dim3(a.B), dim3(kBlock), 0, s, a);
+  const uint32_t grid = launch_grid(a);
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL(sample_general_kernel, dim3(grid), dim3(kBlock), 0, s, a);
   return hipGetLastError();
 }
 
