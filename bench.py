@@ -50,6 +50,15 @@ def parse_args():
     ap.add_argument("--mixed", action="store_true",
                     help="time one call whose rows mix four classes (greedy, top-k, whole vocabulary, "
                          "top-k above the register path) against the sum of one call per class")
+    ap.add_argument("--floor", action="store_true",
+                    help="time the register path's floors on the workload's rows (llmhip_bench_floor: the same "
+                         "grid streaming the rows in and nothing else, and the same grid loading nothing) beside "
+                         "the sampler")
+    ap.add_argument("--decode-window", type=int, default=0, metavar="W",
+                    help="time llmhip_decode_step on the workload with a device history ring whose last W tokens "
+                         "form each row's history")
+    ap.add_argument("--counts", action="store_true",
+                    help="with --decode-window: llmhip_decode_step_counts (incremental count table)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -240,6 +249,120 @@ def bench_mixed(args) -> None:
     sampler.close()
 
 
+def _rotating_sets(w, dev):
+    """Device copies of the workload's logits, rolled by one row each, enough
+    of them that consecutive launches never find their rows in the MALL."""
+    import torch
+
+    set_bytes = w.B * w.ld * 4
+    n_sets = max(2, int(np.ceil(2 * MALL_BYTES / set_bytes)) + 1)
+    base = torch.from_numpy(w.logits).to(dev)
+    return [torch.roll(base, shifts=s, dims=0).contiguous() for s in range(n_sets)]
+
+
+def _event_time_us(stream, fn, warmup, steps):
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps * 1e3
+
+
+def bench_floor(args) -> None:
+    """The register path's floors on the workload's shape: llmhip_bench_floor
+    streaming each row in exactly as the sampling kernel loads it (and nothing
+    else), the same grid loading nothing, and the sampler itself, each back to
+    back over the same rotating input sets."""
+    import torch
+
+    from scriptonait_amd.sampler import Sampler
+    from scriptonait_amd.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload(args.config, B=args.batch)
+    sampler = Sampler(0)
+    stream = torch.cuda.current_stream(dev)
+    sets = _rotating_sets(w, dev)
+    hs = torch.from_numpy(w.hist.view(np.int32)).to(dev) if w.hist is not None else None
+    offs = torch.from_numpy(w.hist_offsets.view(np.int32)).to(dev) if w.hist is not None else None
+    rng = torch.from_numpy(w.rng_seeds.view(np.int64).copy()).to(dev)
+    ids = torch.empty(w.B, dtype=torch.int32, device=dev)
+    out = torch.zeros(w.B, dtype=torch.float32, device=dev)
+    n = len(sets)
+    steps = max(1, min(args.steps, 5000))
+    read_us = _event_time_us(stream, lambda i: sampler.bench_floor(sets[i % n], True, out, V=w.V, stream=stream),
+                             args.warmup, steps)
+    empty_us = _event_time_us(stream, lambda i: sampler.bench_floor(sets[i % n], False, out, V=w.V, stream=stream),
+                              args.warmup, steps)
+    sample_us = _event_time_us(stream, lambda i: sampler.sample_device(sets[i % n], w.params, rng, ids, V=w.V,
+                                                                      hist=hs, hist_offsets=offs, stream=stream),
+                               args.warmup, steps)
+    row_bytes = w.B * w.V * 4
+    print(json.dumps({
+        "metric": "register-path floors, us per launch",
+        "value": read_us, "unit": "us", "higher_is_better": False, "steps": steps, "warmup": args.warmup,
+        "config": {"workload": f"{w.name}: {w.description}", "B": w.B, "V": w.V},
+        "read_floor_us": read_us, "read_floor_gbs": row_bytes / (read_us * 1e-6) / 1e9,
+        "read_floor_frac_of_peak": row_bytes / (read_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+        "dispatch_floor_us": empty_us, "sampler_us": sample_us,
+        "sampler_over_read_floor": sample_us / read_us,
+        "dtype": "f32", "data": f"synthetic ({w.name}, {n} rotating device input sets)",
+    }), flush=True)
+    sampler.close()
+
+
+def bench_decode(args) -> None:
+    """llmhip_decode_step (or, with --counts, llmhip_decode_step_counts) on
+    the workload's rows: each row's ring holds W + 50 uniform ids (capacity
+    W + 1024) and its history is the last W of them; every step appends the
+    drawn id. The count table starts empty, so the first step counts the
+    whole window; the warm-up steps take that cost out of the timed ones."""
+    import torch
+
+    from scriptonait_amd.sampler import Sampler
+    from scriptonait_amd.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload(args.config, B=args.batch)
+    W = args.decode_window
+    cap = W + 1024
+    sampler = Sampler(0)
+    stream = torch.cuda.current_stream(dev)
+    sets = _rotating_sets(w, dev)
+    rs = np.random.default_rng(W)
+    ring = torch.from_numpy(rs.integers(0, w.V, size=(w.B, cap)).astype(np.int32)).to(dev)
+    ln = torch.full((w.B,), W + 50, dtype=torch.int32, device=dev)
+    done = torch.zeros(w.B, dtype=torch.int32, device=dev)
+    rng = torch.from_numpy(w.rng_seeds.view(np.int64).copy()).to(dev)
+    ids = torch.empty(w.B, dtype=torch.int32, device=dev)
+    counts = counted = None
+    if args.counts:
+        counts = torch.zeros((w.B, (w.V + 1) // 2), dtype=torch.int32, device=dev)
+        counted = torch.zeros((w.B, 2), dtype=torch.int32, device=dev)
+    n = len(sets)
+    steps = max(1, min(args.steps, 800))  # the rings hold 1024 - 50 more ids before they wrap past the window
+    us = _event_time_us(stream, lambda i: sampler.decode_step(sets[i % n], w.params, ring, ln, done, W, rng, ids,
+                                                              V=w.V, stream=stream, counts=counts, counted=counted),
+                        min(args.warmup, 100), steps)
+    st = sampler.status()
+    print(json.dumps({
+        "metric": "decode step, us per step",
+        "value": us, "unit": "us", "higher_is_better": False, "steps": steps, "warmup": min(args.warmup, 100),
+        "config": {"workload": f"{w.name}: {w.description}", "B": w.B, "V": w.V, "window": W,
+                   "count_table": bool(args.counts)},
+        "rows_per_s": w.B / (us * 1e-6), "status_flags": st.flags, "handovers": st.handovers,
+        "dtype": "f32", "data": f"synthetic ({w.name}, {n} rotating device input sets, uniform ring ids seed {W})",
+    }), flush=True)
+    sampler.close()
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -257,6 +380,12 @@ def main():
         return
     if args.mixed:
         bench_mixed(args)
+        return
+    if args.floor:
+        bench_floor(args)
+        return
+    if args.decode_window:
+        bench_decode(args)
         return
 
     import torch

@@ -375,6 +375,21 @@ int llmhip_scck_read_params(const uint8_t* bytes, size_t len, const llmhip_scck_
                             uint64_t count, float* out);
 
 /*
+ * Benchmark helper (no reference counterpart): the floors the register-path
+ * kernel is measured against. One launch on `stream` of B workgroups of 1024
+ * threads, the sampling kernel's grid for V <= 32768. With read != 0 each
+ * workgroup loads row b of `logits` (V floats, row stride ld) exactly as the
+ * sampling kernel does (each lane its 16-byte chunks, nontemporal, issued
+ * back to back) and does nothing else: the streaming-read floor of that
+ * access shape. With read == 0 it loads nothing: the dispatch floor. out[B]
+ * is written only for a NaN sum no finite row has (it keeps the loads).
+ * V must be a multiple of 4 up to 32768, ld a multiple of 4 (>= V), and
+ * logits 16-byte aligned; otherwise LLMHIP_ERR_INVALID_ARGUMENT.
+ */
+int llmhip_bench_floor(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld, int read, float* out,
+                       void* stream);
+
+/*
  * Test hooks (no reference counterpart), to exercise the error paths
  * without a kernel fault or hang:
  *   LLMHIP_DEBUG_SPIN_LIMIT  later calls on ctx bound each wait between

@@ -31,6 +31,8 @@ hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s);
 hipError_t launch_take_status(uint32_t* words, hipStream_t s);
+hipError_t launch_read_floor(const float* logits, uint64_t ld, uint32_t B, uint32_t V, int read, float* out,
+                             hipStream_t s);
 hipError_t launch_tied_head(const float* hidden, uint64_t ldh, const float* embed, uint64_t lde, float* logits,
                             uint64_t ldl, uint32_t B, uint32_t V, uint32_t h, hipStream_t s);
 }  // namespace llmhip
@@ -593,6 +595,20 @@ int llmhip_seen_tokens(llmhip_ctx* ctx, const uint32_t* tokens, size_t n, size_t
   Device d(ctx->device);
   if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
   HIP_TRY(launch_seen_bits(tokens, n, (uint32_t)V, seen_bits, static_cast<hipStream_t>(stream)));
+  return LLMHIP_OK;
+}
+
+int llmhip_bench_floor(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld, int read, float* out,
+                       void* stream) {
+  if (!ctx) return arg_fail("ctx is null");
+  if (B == 0 || B > 0x7fffffffu) return arg_fail("B must be in 1 .. 2^31-1");
+  if (V == 0 || V > kMaxFastV || V % 4 != 0) return arg_fail("V must be a multiple of 4 in 4 .. 32768");
+  if (ld < V || ld % 4 != 0) return arg_fail("ld must be a multiple of 4, at least V");
+  if (!logits || reinterpret_cast<uintptr_t>(logits) % 16 != 0) return arg_fail("logits must be 16-byte aligned");
+  if (!out) return arg_fail("out is null");
+  Device d(ctx->device);
+  if (!d.ok) return hip_fail(hipErrorInvalidDevice, "hipSetDevice");
+  HIP_TRY(launch_read_floor(logits, ld, (uint32_t)B, (uint32_t)V, read, out, static_cast<hipStream_t>(stream)));
   return LLMHIP_OK;
 }
 

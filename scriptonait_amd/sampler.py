@@ -54,6 +54,7 @@ EXPORTED_SYMBOLS = (
     "llmhip_ctx_debug",
     "llmhip_scck_parse",
     "llmhip_scck_read_params",
+    "llmhip_bench_floor",
 )
 KSTATUS_SYNC_TIMEOUT = 1
 DEBUG_SPIN_LIMIT = 1
@@ -128,6 +129,8 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.llmhip_ctx_debug.argtypes = [vp, ctypes.c_int, u32]
     lib.llmhip_seen_tokens.restype = ctypes.c_int
     lib.llmhip_seen_tokens.argtypes = [vp, vp, sz, sz, vp, vp]
+    lib.llmhip_bench_floor.restype = ctypes.c_int
+    lib.llmhip_bench_floor.argtypes = [vp, vp, sz, sz, sz, ctypes.c_int, vp, vp]
     _lib = lib
     return lib
 
@@ -385,6 +388,18 @@ class Sampler:
                 dp(rng_state), dp(out_ids), stream.cuda_stream)
         _check(self.lib, status)
 
+
+    def bench_floor(self, logits, read: bool, out, V: Optional[int] = None, stream=None) -> None:
+        """llmhip_bench_floor on a [B, ld] float32 CUDA tensor: one launch of
+        the register path's grid that only streams the rows in (read) or
+        loads nothing; `out` is a [B] float32 CUDA tensor."""
+        import torch
+
+        B, ld = logits.shape
+        if stream is None:
+            stream = torch.cuda.current_stream(logits.device)
+        _check(self.lib, self.lib.llmhip_bench_floor(self.ctx, logits.data_ptr(), B, ld if V is None else V, ld,
+                                                     1 if read else 0, out.data_ptr(), stream.cuda_stream))
 
     def status(self, stream=None) -> LlmhipStatus:
         """llmhip_ctx_status: waits for `stream` (default: the null stream),
