@@ -31,6 +31,7 @@ hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s);
 hipError_t launch_take_status(uint32_t* words, hipStream_t s);
+hipError_t launch_stream(const SampleArgs& a, bool vec, hipStream_t s);
 hipError_t launch_read_floor(const float* logits, uint64_t ld, uint32_t B, uint32_t V, int read, float* out,
                              hipStream_t s);
 hipError_t launch_tied_head(const float* hidden, uint64_t ldh, const float* embed, uint64_t lde, float* logits,
@@ -111,6 +112,7 @@ struct llmhip_ctx {
   DevBuf head_logits;            // the tied head's logits when the caller does not take them
   uint32_t spin_limit = kSpinLimit;  // bound of the kernels' waits between wavefronts
   uint32_t* noalloc = nullptr;   // this device's address of the file-scope `scratch` (null: lookup failed)
+  uint32_t cus = 0;              // the device's compute units (persistent launches take one workgroup each)
   // staging of the host entry
   DevBuf logits, hist, hoff, allowed, rng, ids, probs, kept;
 };
@@ -229,16 +231,18 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   uint32_t row_cls[128] = {};  // each row's class index (SampleArgs::row_cls), for calls of <= kRowClsRows rows
   for (size_t b = 0; b < (params_stride ? B : 1); ++b) {
     const llmhip_params& p = params_host[b * params_stride];
-    const uint32_t c = row_class(p, (uint32_t)V);
+    const uint32_t c = route_class(p, (uint32_t)V);
     classes |= c;
     bigk = bigk || (c == kClassTopK && p.top_k > 64u);
     if (b < kRowClsRows) row_cls[b >> 4] |= (uint32_t)__builtin_ctz(c) << ((b & 15u) * 2u);
   }
   const bool fast_ok = V <= kMaxFastV;
   const uint32_t fast_mask = fast_ok ? (classes & (kClassGreedy | kClassTopK)) : 0u;
-  // Full-vocabulary rows take the bucketed exact-fold kernel.
+  // Top-k rows past the register path's V stream through the persistent
+  // kernel; full-vocabulary rows take the bucketed exact-fold kernel.
+  const uint32_t stream_mask = fast_ok ? 0u : (classes & kClassTopK);
   const uint32_t vocab_mask = classes & kClassVocab;
-  const uint32_t general_mask = classes & ~fast_mask & ~vocab_mask;
+  const uint32_t general_mask = classes & ~fast_mask & ~vocab_mask & ~stream_mask;
 
   // The fast kernel may hand a row to the general path, so scratch is
   // always sized for the batch.
@@ -286,6 +290,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   a.spin_limit = ctx->spin_limit;
   a.scratch = scr;
   a.scratch_row_words = row_words;
+  a.cus = ctx->cus;
   // Rows of several classes: one launch per class, and each launch's
   // workgroups skip the rows of the others before reading them.
   if (params_stride && B <= kRowClsRows && __builtin_popcount(classes) > 1) {
@@ -309,6 +314,12 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
     }
     a.row_class_mask = fast_mask;
     HIP_TRY(a.counts ? launch_fast_counts(a, vec, bigk, s) : launch_fast(a, vec, bigk, s));
+  }
+  if (stream_mask) {
+    // A row's last float4 may pass V (the stride is a multiple of 4).
+    const bool svec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0);
+    a.row_class_mask = stream_mask;
+    HIP_TRY(launch_stream(a, svec, s));
   }
   if (vocab_mask) {
     a.row_class_mask = vocab_mask;
@@ -414,6 +425,9 @@ int llmhip_ctx_create(int device, llmhip_ctx** out_ctx) {
   llmhip_ctx* ctx = new llmhip_ctx();
   ctx->device = device;
   ctx->noalloc = noalloc_scratch(device);
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+    ctx->cus = (uint32_t)cus;
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

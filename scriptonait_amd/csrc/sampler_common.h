@@ -114,15 +114,19 @@ struct SampleArgs {
   // and each finds its row's class from the row's parameters.
   uint32_t row_cls_on;
   uint32_t row_cls[128];
+  // Persistent launches (the streaming path): rows of the launch (its
+  // workgroups take rows j, j + gridDim.x, ...), and the device's CUs.
+  uint32_t launch_rows;
+  uint32_t cus;
 };
 constexpr uint32_t kRowClsRows = 16u * 128u;
 
-// The row a workgroup samples: blockIdx.x, or, with the class table,
-// the blockIdx.x-th row (in row order) of the launch's classes. Every
-// thread of the workgroup calls it (full waves); lane l of each wave reads
-// table words 2l and 2l+1 (rows 32l .. 32l+31).
-__device__ __forceinline__ uint32_t launch_row(const SampleArgs& a) {
-  if (!a.row_cls_on) return blockIdx.x;
+// Row j of a launch: j, or, with the class table, the j-th row (in row
+// order) of the launch's classes. Every thread of the workgroup calls it
+// (full waves); lane l of each wave reads table words 2l and 2l+1 (rows
+// 32l .. 32l+31).
+__device__ __forceinline__ uint32_t launch_row_at(const SampleArgs& a, uint32_t j) {
+  if (!a.row_cls_on) return j;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t w0 = a.row_cls[2u * lane], w1 = a.row_cls[2u * lane + 1u];
   uint32_t m0 = 0u, m1 = 0u;  // bit 2i: field i holds one of the launch's classes
@@ -137,7 +141,6 @@ __device__ __forceinline__ uint32_t launch_row(const SampleArgs& a) {
   const uint32_t incl = wave_incl_scan(n);
   // The grid counts the launch's rows below B only, and the zero fields
   // past B come after them in order, so the j-th match is a row below B.
-  const uint32_t j = blockIdx.x;
   const uint32_t L = (uint32_t)__builtin_ctzll(__ballot(incl > j));
   uint32_t r = j - (readlane_u32(incl, L) - readlane_u32(n, L));
   uint32_t m = readlane_u32(m0, L), base = 32u * L;
@@ -150,6 +153,9 @@ __device__ __forceinline__ uint32_t launch_row(const SampleArgs& a) {
   for (; r; --r) m &= m - 1u;
   return base + ((uint32_t)__builtin_ctz(m) >> 1);
 }
+
+// The row workgroup blockIdx.x samples (one workgroup per row of the launch).
+__device__ __forceinline__ uint32_t launch_row(const SampleArgs& a) { return launch_row_at(a, blockIdx.x); }
 
 // Workgroups of a launch over the classes in a.row_class_mask (host side).
 inline uint32_t launch_grid(const SampleArgs& a) {
@@ -360,6 +366,26 @@ __host__ __device__ __forceinline__ uint32_t row_class(const llmhip_params& p, u
   if (p.top_k > 0 && p.top_k < V && p.top_k <= kMaxFastK) return kClassTopK;
   if (p.top_k == 0 || p.top_k >= V) return kClassVocab;
   return kClassFull;
+}
+
+// The streaming path (top-k rows past kMaxFastV) lists about 1.2 K values
+// per 32768 of the row (its threshold comes from the row's first 32768
+// values) in a list of kStreamCand: it takes a row when that fits with a
+// margin, and when the penalty is at least 1 (one below 1 can raise a value
+// past the threshold).
+constexpr uint32_t kStreamSpan = 32768;
+constexpr uint32_t kStreamCand = 4096;
+__host__ __device__ __forceinline__ bool stream_takes(const llmhip_params& p, uint32_t V) {
+  const uint32_t parts = (V + kStreamSpan - 1u) / kStreamSpan;
+  return (uint64_t)p.top_k * parts * 5u <= (uint64_t)kStreamCand * 4u && p.repetition_penalty >= 1.0f;
+}
+
+// The path a row is routed to: its class, except that a top-k row past the
+// register path that the streaming path does not take goes with the
+// kClassFull rows (the sorting path, which selects any K <= kSelCap).
+__host__ __device__ __forceinline__ uint32_t route_class(const llmhip_params& p, uint32_t V) {
+  const uint32_t c = row_class(p, V);
+  return c == kClassTopK && V > kMaxFastV && !stream_takes(p, V) ? kClassFull : c;
 }
 
 // Top-k rows of the sorting path with K up to kSelCap are selected and

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(kBlock) void sample_general_kernel(SampleArgs a) {
   __shared__ GenLds L;
   const uint32_t b = launch_row(a);
   if (b >= a.B) return;
-  if (!a.row_cls_on && !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  if (!a.row_cls_on && !(route_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   general_row(a, b, L, false);
 }
 
@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
   } L;
   const uint32_t b = launch_row(a);
   if (b >= a.B) return;
-  if (!a.row_cls_on && !(row_class(load_params(a, b), a.V) & a.row_class_mask)) return;
+  if (!a.row_cls_on && !(route_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   const bool vec4 = (reinterpret_cast<uintptr_t>(a.logits) % 16u == 0u) && (a.ld % 4u == 0u);
   if (!vocab_row(a, b, L.v, vec4)) {
     if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);

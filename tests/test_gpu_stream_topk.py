@@ -1,0 +1,161 @@
+"""GPU: top-k rows of vocabularies past the register path (V > 32768), which
+the streaming kernel samples (one persistent workgroup per CU, each row read
+once through registers), against the oracle.
+
+Every id, kept count and RNG state must equal the oracle's (no tie
+allowance), and the probabilities must equal its bits. The hand-over count
+says how many rows the kernel passed to the sorting path: rows whose K the
+list holds and whose penalty is at least 1 pass none, unless their threshold
+is not bounded (tie runs, crowded bins), which the fallback tests force.
+Rows past the number of CUs exercise the persistent loop (a workgroup takes
+rows j, j + grid, ...), with the next row's loads issued before the current
+row's tail.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from scriptonait_amd.workloads import PARAMS_DTYPE, make_params, make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+def _device_run(sampler, w, params, allowed=None, want_probs=True):
+    """llmhip_sample_device on device copies of the workload (its own row
+    stride: config 4 keeps 50260, a multiple of 4); returns ids, kept, RNG
+    states, probabilities and the hand-over count."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    sampler.status()
+    lg = torch.from_numpy(np.ascontiguousarray(w.logits)).to(dev)
+    hs = offs = None
+    if w.hist is not None:
+        hs = torch.from_numpy(w.hist.view(np.int32)).to(dev)
+        offs = torch.from_numpy(w.hist_offsets.view(np.int32)).to(dev)
+    al = None if allowed is None else torch.from_numpy(allowed).to(dev)
+    rng = torch.from_numpy(w.rng_seeds.view(np.int64).copy()).to(dev)
+    ids = torch.full((w.B,), -1, dtype=torch.int32, device=dev)
+    kept = torch.full((w.B,), -1, dtype=torch.int32, device=dev)
+    probs = torch.full((w.B, w.V), -1.0, dtype=torch.float32, device=dev) if want_probs else None
+    sampler.sample_device(lg, params, rng, ids, V=w.V, hist=hs, hist_offsets=offs, allowed=al, out_probs=probs,
+                          out_kept=kept)
+    torch.cuda.synchronize()
+    return dict(ids=ids.cpu().numpy().view(np.uint32), kept=kept.cpu().numpy().view(np.uint32),
+                rng=rng.cpu().numpy().view(np.uint64), probs=None if probs is None else probs.cpu().numpy(),
+                handovers=sampler.status().handovers)
+
+
+def _check(g, w, params, label, allowed=None, want_probs=True):
+    o = oracle.sample_batch(w.logits, params, w.rng_seeds, w.hist, w.hist_offsets, V=w.V, allowed=allowed,
+                            threads=8, want_probs=want_probs)
+    bad = np.nonzero(g["ids"] != o.ids)[0]
+    assert bad.size == 0, f"{label}: ids differ at rows {bad[:8]} gpu={g['ids'][bad[:8]]} oracle={o.ids[bad[:8]]}"
+    bad = np.nonzero(g["kept"] != o.kept)[0]
+    assert bad.size == 0, f"{label}: kept differs at rows {bad[:8]}"
+    assert np.array_equal(g["rng"], o.rng_state), f"{label}: rng state differs"
+    if want_probs:
+        assert np.array_equal(g["probs"].view(np.uint32), o.probs.view(np.uint32)), f"{label}: probability bits differ"
+
+
+@pytest.mark.parametrize("k", [1, 40, 50, 64, 65, 300, 1000, 1600])
+def test_config4_rows_by_k(sampler, k):
+    """Config 4's data (V = 50257, stride 50260) with top_k overridden; 300
+    rows, so the persistent workgroups take more than one row each."""
+    w = make_workload(4, B=300)
+    prm = make_params(1.0, k, 0.98, 0.0, 1.0)
+    print(f"config 4 B=300 k={k}", flush=True)
+    g = _device_run(sampler, w, prm)
+    _check(g, w, prm, f"config4 k={k}")
+    assert g["handovers"] == 0
+
+
+@pytest.mark.parametrize("k", [40, 50, 500])
+def test_config5_rows_with_history(sampler, k):
+    """Config 5's data (V = 131072, Gumbel logits, Zipf histories of 2048 ids,
+    penalty 1.3) with top_k overridden: eight pieces per row, and penalized
+    values taken only where they can reach the threshold."""
+    w = make_workload(5, B=300)
+    prm = make_params(0.9, k, 1.0, 0.02, 1.3)
+    print(f"config 5 B=300 k={k}", flush=True)
+    g = _device_run(sampler, w, prm)
+    _check(g, w, prm, f"config5 k={k}")
+    assert g["handovers"] == 0
+
+
+def test_history_of_each_rows_top_ids(sampler):
+    """V = 50257 rows whose history repeats each row's own top 8 ids (the top
+    one 300 times): the penalties decide the top K, and the early stop of the
+    penalty loop must not change a value that stays above the threshold."""
+    w = make_workload(4, B=64)
+    rows = []
+    for b in range(w.B):
+        order = np.argsort(-w.logits[b, :w.V], kind="stable")
+        rows.append(np.concatenate([np.full(300, order[0]), np.repeat(order[1:8], 5)]).astype(np.uint32))
+    w.hist = np.concatenate(rows)
+    w.hist_offsets = np.zeros(w.B + 1, dtype=np.uint32)
+    w.hist_offsets[1:] = np.cumsum([len(r) for r in rows])
+    for rp in (1.05, 1.0001):
+        prm = make_params(0.8, 40, 0.95, 0.01, rp)
+        g = _device_run(sampler, w, prm)
+        _check(g, w, prm, f"top ids in history rp={rp}")
+        assert g["handovers"] == 0
+
+
+def test_mask_and_penalty(sampler):
+    """An allowed mask that removes every third id (EOS stays allowed) and a
+    uniform history, on the host entry (dense rows: V = 50257 is not a
+    multiple of 4, so the rows are read a float at a time)."""
+    w = make_workload(4, B=40)
+    rs = np.random.default_rng(11)
+    w.hist = rs.integers(0, w.V, size=w.B * 700).astype(np.uint32)
+    w.hist_offsets = (np.arange(w.B + 1) * 700).astype(np.uint32)
+    allowed = (np.arange(w.V) % 3 != 1).astype(np.uint8)
+    prm = make_params(0.7, 64, 0.9, 0.05, 1.2)
+    sampler.status()
+    g = sampler.sample_host(w.logits, prm, w.rng_seeds, w.hist, w.hist_offsets, allowed=allowed, V=w.V,
+                            want_probs=True)
+    hand = sampler.status().handovers
+    _check(dict(ids=g.ids, kept=g.kept, rng=g.rng_state, probs=g.probs), w, prm, "mask and penalty",
+           allowed=allowed)
+    assert hand == 0
+
+
+def test_per_row_params_and_other_classes(sampler):
+    """Per-row parameters at V = 50257 mixing every class: greedy rows, top-k
+    rows of the streaming kernel, a K it sends on to the sorting path, rows
+    with a penalty below 1 (also sent on), and full-vocabulary rows."""
+    w = make_workload(4, B=90)
+    prm = np.zeros(w.B, dtype=PARAMS_DTYPE)
+    kinds = [(0.0, 50, 0.9, 0.1, 1.2), (1.0, 50, 0.9, 0.1, 1.2), (0.8, 40, 0.95, 0.0, 1.0),
+             (1.2, 3000, 0.9, 0.0, 1.0), (0.9, 64, 0.9, 0.0, 0.9), (1.0, 0, 0.98, 0.0, 1.0)]
+    for b in range(w.B):
+        prm[b] = kinds[b % len(kinds)]
+    g = _device_run(sampler, w, prm)
+    _check(g, w, prm, "mixed per-row params")
+
+
+@pytest.mark.parametrize("V", [32769, 32772, 40000, 65537, 98304])
+def test_vocab_sizes_around_the_pieces(sampler, V):
+    """Vocabularies just past the register path and around the pieces'
+    edges (16384 values each), on both entries (dense host rows, and device
+    rows of config 4's padded stride)."""
+    w = make_workload(4, B=24, V=V)
+    prm = make_params(0.9, 50, 0.95, 0.02, 1.0)
+    g = _device_run(sampler, w, prm)
+    _check(g, w, prm, f"device V={V}")
+    h = sampler.sample_host(w.logits, prm, w.rng_seeds, None, None, V=V, want_probs=True)
+    _check(dict(ids=h.ids, kept=h.kept, rng=h.rng_state, probs=h.probs), w, prm, f"host V={V}")
+
+
+def test_more_rows_than_the_class_table(sampler):
+    """2100 rows (past the 2048 rows of the host-made class table): the
+    persistent workgroups find each row's class from its parameters and skip
+    the other launches' rows."""
+    w = make_workload(4, B=2100, V=40000)
+    prm = np.zeros(w.B, dtype=PARAMS_DTYPE)
+    kinds = [(0.0, 50, 0.9, 0.1, 1.0), (1.0, 50, 0.9, 0.1, 1.0), (0.7, 2, 1.0, 0.0, 1.0)]
+    for b in range(w.B):
+        prm[b] = kinds[b % 3]
+    g = _device_run(sampler, w, prm, want_probs=False)
+    _check(g, w, prm, "2100 rows", want_probs=False)
