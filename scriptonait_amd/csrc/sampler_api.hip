@@ -31,7 +31,7 @@ hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s);
 hipError_t launch_take_status(uint32_t* words, hipStream_t s);
-hipError_t launch_stream(const SampleArgs& a, bool vec, hipStream_t s);
+hipError_t launch_stream(const SampleArgs& a, bool vec, bool bigk, hipStream_t s);
 hipError_t launch_read_floor(const float* logits, uint64_t ld, uint32_t B, uint32_t V, int read, float* out,
                              hipStream_t s);
 hipError_t launch_tied_head(const float* hidden, uint64_t ldh, const float* embed, uint64_t lde, float* logits,
@@ -319,7 +319,7 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
     // A row's last float4 may pass V (the stride is a multiple of 4).
     const bool svec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (ld % 4 == 0);
     a.row_class_mask = stream_mask;
-    HIP_TRY(launch_stream(a, svec, s));
+    HIP_TRY(launch_stream(a, svec, bigk, s));
   }
   if (vocab_mask) {
     a.row_class_mask = vocab_mask;

@@ -56,8 +56,10 @@ constexpr uint32_t kSMaxDistinct = 3072;     // distinct history ids the hash ta
 constexpr uint32_t kSBits = 4096;            // words of the history filter (bit id mod 2^17)
 constexpr uint32_t kSEmpty = 0xffffffffu;
 
+constexpr uint32_t kSPend = 512;             // listed values waiting for their penalty
+
 // misc[] slots
-enum : uint32_t { kSCandN = 0, kSDistinct = 1, kSFull = 2, kSMisc = 4 };
+enum : uint32_t { kSCandN = 0, kSDistinct = 1, kSFull = 2, kSPendN = 3, kSMisc = 4 };
 
 struct StreamLds {
   __attribute__((aligned(16))) uint32_t coarse[kCoarseBins];
@@ -67,6 +69,7 @@ struct StreamLds {
   uint32_t hkey[kSHash];
   uint32_t hcnt[kSHash];
   uint32_t hbits[kSBits];
+  uint64_t pend[kSPend];  // (raw value bits, id) of marked values at or above the threshold
   uint32_t skey[64];
   uint32_t sid[64];
   __attribute__((aligned(16))) float tail[64];
@@ -127,7 +130,12 @@ __device__ __forceinline__ void stream_load(float (&buf)[kSNS * 4], const float*
 
 // The rows of one launch (all threads). VEC: 16-byte aligned rows with a
 // stride of a multiple of 4 floats (a row's last float4 may pass V, not ld).
-template <bool VEC>
+// FULL: the call has an allowed mask or is a decode step (a ring, maybe a
+// count table); the other calls run a variant compiled without that code,
+// whose loop keeps fewer values live. BIGK: some row of the launch has
+// K > 64; without it the kernel holds only the register rank and tail, and a
+// row listing more than 512 values is handed over.
+template <bool VEC, bool FULL, bool BIGK>
 __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds& U) {
   StreamLds& L = U.s;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -153,7 +161,7 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
     r.P = load_params(a, rb);
     r.rng0 = a.rng_state[rb];
     r.h0 = r.h1 = r.done = 0u;
-    if (a.ring_cap) {
+    if (FULL && a.ring_cap) {
       r.h0 = a.ring_len[rb];
       r.h1 = ring_avail(a, rb, r.h0);
       r.done = a.done ? a.done[rb] : 0u;
@@ -187,7 +195,8 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
     if (!a.row_cls_on && !(route_class(P, V) & a.row_class_mask)) outcome = 3u;
 
     const uint32_t len_b = ri.h0;
-    const HistRow hr = hist_row(a, b, ri.h0, ri.h1);
+    const HistRow hr = FULL ? hist_row(a, b, ri.h0, ri.h1)
+                            : HistRow{a.hist + ri.h0, 0u, 0u, ri.h1 > ri.h0 ? ri.h1 - ri.h0 : 0u};
     LLMHIP_MARK(0);
     if (outcome == 0u && ri.done) {
       // Decode-step mode: a finished generation is skipped (no draw).
@@ -200,7 +209,7 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
     // The count table is kept current for the next step; this path counts
     // the window itself.
     bool counts_moved = false;
-    if (outcome == 0u && a.ring_cap && a.counts) {
+    if (FULL && outcome == 0u && a.ring_cap && a.counts) {
       counts_advance_all(a, b, len_b, hr.H);
       counts_moved = true;
     }
@@ -246,7 +255,7 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
     //    past V and where the allowed mask excludes the id (-inf in the
     //    reference, so never listed); pm, set for ids in the history. Then
     //    the group maxima of the values in neither.
-    const bool masked = a.allowed || a.allowed_bits;
+    const bool masked = FULL && (a.allowed || a.allowed_bits);
     auto prep = [&](uint32_t p, uint32_t& xm) __attribute__((always_inline)) -> uint32_t {
       const uint32_t tid = opaque_tid();
       uint32_t pm = 0u;
@@ -310,17 +319,17 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
         if (o < kSCand) L.list[o] = ((uint64_t)__float_as_uint(v) << 32) | i;
         ++o;
       }
+      // Marked values wait in their own list: their penalty is applied once
+      // the row is streamed (a penalty loop here would weigh on every
+      // piece's code).
       for (uint32_t h = pen; h != 0u; h &= h - 1u) {
         const uint32_t e = (uint32_t)__builtin_ctz(h);
         float v = buf[0];
 #pragma unroll
         for (int q = 1; q < (int)kSNS * 4; ++q) v = e == (uint32_t)q ? buf[q] : v;
         const uint32_t i = 4u * (p * kSPieceQ + (e >> 2) * kBlock + tid) + (e & 3u);
-        v = apply_penalty_above(v, stream_count(L, i), rp, tf);
-        if (v >= tf) {
-          const uint32_t q = atomicAdd(&L.misc[kSCandN], 1u);
-          if (q < kSCand) L.list[q] = ((uint64_t)__float_as_uint(v) << 32) | i;
-        }
+        const uint32_t q = atomicAdd(&L.misc[kSPendN], 1u);
+        if (q < kSPend) L.pend[q] = ((uint64_t)__float_as_uint(v) << 32) | i;
       }
     };
 
@@ -371,9 +380,30 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
         fetched = true;
         LLMHIP_MARK(5);
         lds_barrier();
+        // The marked values' penalties (generate.rs:343-352), stopping once
+        // a value is below the threshold (exact for rp >= 1).
+        const uint32_t npend = L.misc[kSPendN];
+        if (npend != 0u) {
+          if (npend > kSPend) {
+            outcome = 1u;
+          } else {
+            for (uint32_t q = tid; q < npend; q += kBlock) {
+              const uint64_t r = L.pend[q];
+              const uint32_t i = (uint32_t)r;
+              const float v = apply_penalty_above(__uint_as_float((uint32_t)(r >> 32)), stream_count(L, i), rp, tf);
+              if (v >= tf) {
+                const uint32_t o = atomicAdd(&L.misc[kSCandN], 1u);
+                if (o < kSCand) L.list[o] = ((uint64_t)__float_as_uint(v) << 32) | i;
+              }
+            }
+            lds_barrier();
+          }
+        }
         n = L.misc[kSCandN];
         // At least K: the K group maxima above t0 are listed.
-        if (n > kSCand || n < K) outcome = 1u;
+        // (A launch without BIGK never holds K > 64; that test only keeps
+        // its 64-entry rank output in bounds.)
+        if (n > (BIGK ? kSCand : 512u) || n < K || (!BIGK && K > 64u)) outcome = 1u;
       }
     }
 
@@ -392,7 +422,7 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
       }
       lds_barrier();
       LLMHIP_MARK(12);
-      if (K <= 64u && n <= 512u) {
+      if (!BIGK || (K <= 64u && n <= 512u)) {
         if (n <= 128u) {
           rank_in_regs<2>(L.list, n, K, wave, lane, L.skey, L.sid);
         } else if (n <= 256u) {
@@ -409,7 +439,7 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
                           st_next, L.exptab, L.tail);
           LLMHIP_MARK(7);
         }
-      } else {
+      } else if constexpr (BIGK) {
         const uint64_t* srt = n <= kBlock        ? sort_desc_lds<1>(L.list, L.tmp, n)
                               : n <= 2u * kBlock ? sort_desc_lds<2>(L.list, L.tmp, n)
                                                  : sort_desc_lds<4>(L.list, L.tmp, n);
