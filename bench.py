@@ -320,10 +320,13 @@ def bench_floor(args) -> None:
 
 def bench_decode(args) -> None:
     """llmhip_decode_step (or, with --counts, llmhip_decode_step_counts) on
-    the workload's rows: each row's ring holds W + 50 uniform ids (capacity
-    W + 1024) and its history is the last W of them; every step appends the
-    drawn id. The count table starts empty, so the first step counts the
-    whole window; the warm-up steps take that cost out of the timed ones."""
+    the workload's rows as a decode loop: each row's ring starts with a
+    50-token prompt of uniform ids (capacity W + 1024), every step appends
+    the drawn id, and the history is the last W tokens. The untimed warm-up
+    runs W steps (at least --warmup), so the timed steps' windows hold the
+    generations' own draws: a row's recent top candidates, which the penalty
+    pushes below the register path's speculative threshold on some rows.
+    No generation ends (the end-of-text id is set past the vocabulary)."""
     import torch
 
     from scriptonait_amd.sampler import Sampler
@@ -337,8 +340,9 @@ def bench_decode(args) -> None:
     stream = torch.cuda.current_stream(dev)
     sets = _rotating_sets(w, dev)
     rs = np.random.default_rng(W)
-    ring = torch.from_numpy(rs.integers(0, w.V, size=(w.B, cap)).astype(np.int32)).to(dev)
-    ln = torch.full((w.B,), W + 50, dtype=torch.int32, device=dev)
+    ring = torch.zeros((w.B, cap), dtype=torch.int32, device=dev)
+    ring[:, :50] = torch.from_numpy(rs.integers(0, w.V, size=(w.B, 50)).astype(np.int32)).to(dev)
+    ln = torch.full((w.B,), 50, dtype=torch.int32, device=dev)
     done = torch.zeros(w.B, dtype=torch.int32, device=dev)
     rng = torch.from_numpy(w.rng_seeds.view(np.int64).copy()).to(dev)
     ids = torch.empty(w.B, dtype=torch.int32, device=dev)
@@ -347,18 +351,22 @@ def bench_decode(args) -> None:
         counts = torch.zeros((w.B, (w.V + 1) // 2), dtype=torch.int32, device=dev)
         counted = torch.zeros((w.B, 2), dtype=torch.int32, device=dev)
     n = len(sets)
-    steps = max(1, min(args.steps, 800))  # the rings hold 1024 - 50 more ids before they wrap past the window
+    no_eos = 0xFFFFFFFF
+    steps = max(1, min(args.steps, 1000))
+    warmup = max(args.warmup, W)
     us = _event_time_us(stream, lambda i: sampler.decode_step(sets[i % n], w.params, ring, ln, done, W, rng, ids,
-                                                              V=w.V, stream=stream, counts=counts, counted=counted),
-                        min(args.warmup, 100), steps)
+                                                              V=w.V, eos_id=no_eos, stream=stream, counts=counts,
+                                                              counted=counted),
+                        warmup, steps)
     st = sampler.status()
     print(json.dumps({
         "metric": "decode step, us per step",
-        "value": us, "unit": "us", "higher_is_better": False, "steps": steps, "warmup": min(args.warmup, 100),
+        "value": us, "unit": "us", "higher_is_better": False, "steps": steps, "warmup": warmup,
         "config": {"workload": f"{w.name}: {w.description}", "B": w.B, "V": w.V, "window": W,
                    "count_table": bool(args.counts)},
         "rows_per_s": w.B / (us * 1e-6), "status_flags": st.flags, "handovers": st.handovers,
-        "dtype": "f32", "data": f"synthetic ({w.name}, {n} rotating device input sets, uniform ring ids seed {W})",
+        "dtype": "f32", "data": f"synthetic ({w.name}, {n} rotating device input sets; rings of a 50-id "
+                                f"uniform prompt (seed {W}) and the generations' own draws)",
     }), flush=True)
     sampler.close()
 

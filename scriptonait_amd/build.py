@@ -25,7 +25,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libllmhip_sampler.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["sampler_kernels.hip", "fast_nch8.hip", "fast_nch_small.hip", "fast_counts.hip", "fast_counts8.hip",
+SOURCES = ["sampler_kernels.hip", "vocab_full.hip", "vocab_plain.hip", "fast_nch8.hip", "fast_nch_small.hip", "fast_counts.hip", "fast_counts8.hip",
            "fast_counts_small.hip", "tied_head.hip", "bench_floor.hip", "stream_topk.hip", "stream_topk_bigk.hip", "sampler_api.hip", "scck_reader.cpp"]
 ARCH = "gfx950"
 

@@ -27,7 +27,7 @@ namespace llmhip {
 hipError_t launch_fast(const SampleArgs& a, bool vec, bool bigk, hipStream_t s);
 hipError_t launch_fast_counts(const SampleArgs& a, bool vec, bool bigk, hipStream_t s);
 hipError_t launch_general(const SampleArgs& a, hipStream_t s);
-hipError_t launch_vocab(const SampleArgs& a, hipStream_t s);
+hipError_t launch_vocab(const SampleArgs& a, bool plain, hipStream_t s);
 hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s);
 hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s);
 hipError_t launch_take_status(uint32_t* words, hipStream_t s);
@@ -228,12 +228,14 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   }
   uint32_t classes = 0;
   bool bigk = false;  // some top-k row of the register path has K > 64
+  bool penalized = false;  // some row has a repetition penalty (and the call a history)
   uint32_t row_cls[128] = {};  // each row's class index (SampleArgs::row_cls), for calls of <= kRowClsRows rows
   for (size_t b = 0; b < (params_stride ? B : 1); ++b) {
     const llmhip_params& p = params_host[b * params_stride];
     const uint32_t c = route_class(p, (uint32_t)V);
     classes |= c;
     bigk = bigk || (c == kClassTopK && p.top_k > 64u);
+    penalized = penalized || p.repetition_penalty != 1.0f;
     if (b < kRowClsRows) row_cls[b >> 4] |= (uint32_t)__builtin_ctz(c) << ((b & 15u) * 2u);
   }
   const bool fast_ok = V <= kMaxFastV;
@@ -323,7 +325,8 @@ int enqueue(llmhip_ctx* ctx, const float* logits, size_t B, size_t V, size_t ld,
   }
   if (vocab_mask) {
     a.row_class_mask = vocab_mask;
-    HIP_TRY(launch_vocab(a, s));
+    const bool plain = !a.allowed && !a.allowed_bits && !a.ring && !(penalized && a.hist);
+    HIP_TRY(launch_vocab(a, plain, s));
   }
   if (general_mask) {
     a.row_class_mask = general_mask;

@@ -1,8 +1,9 @@
 // gfx950 kernels of the decode-time sampler.
 //
 // One 1024-thread workgroup (16 wave64s) samples one row, so a batch of B
-// rows is B workgroups and B=256 fills the 256 CUs of an MI355X once. Three
-// kernels share the row semantics of crates/llm-core/src/generate.rs:325-420:
+// rows is B workgroups and B=256 fills the 256 CUs of an MI355X once (the
+// streaming kernel's workgroups take several rows each). Four kernels share
+// the row semantics of crates/llm-core/src/generate.rs:325-420:
 //
 //  * sample_fast_kernel (V <= 32768, 0 < top_k <= 4096, and greedy rows):
 //    the row stays in registers and the sample is decided while it streams
@@ -11,10 +12,15 @@
 //
 //  * sample_vocab_kernel (top_k == 0 or top_k >= V: the whole vocabulary
 //    is kept): the reference's three folds replayed exactly over value
-//    buckets, without sorting the row (vocab_row.h).
+//    buckets, without sorting the row (vocab_row.h; compiled in
+//    vocab_full.hip and vocab_plain.hip).
 //
-//  * sample_general_kernel (top-k rows the fast kernel does not take, V >
-//    32768 or top_k > 4096, and rows the other two hand over): an LDS select
+//  * sample_stream_kernel (top-k rows past the fast kernel's V): the row
+//    streamed through registers once (stream_row.h; compiled in
+//    stream_topk.hip and stream_topk_bigk.hip).
+//
+//  * sample_general_kernel (top-k rows neither the fast nor the streaming
+//    kernel takes, top_k > 4096, and rows the others hand over): an LDS select
 //    of the top K, or a stable LSD radix sort of (key, id) pairs in per-row
 //    HBM scratch, then the same sequential tail (general_row.h).
 #include <algorithm>
@@ -24,7 +30,6 @@
 #include "fast_row.h"
 #include "general_row.h"
 #include "sampler_common.h"
-#include "vocab_row.h"
 #include "wave_ops.h"
 
 namespace llmhip {
@@ -35,27 +40,6 @@ __global__ __launch_bounds__(kBlock) void sample_general_kernel(SampleArgs a) {
   if (b >= a.B) return;
   if (!a.row_cls_on && !(route_class(load_params(a, b), a.V) & a.row_class_mask)) return;
   general_row(a, b, L, false);
-}
-
-// ---------------------------------------------------------------------------
-// Full-vocabulary kernel (vocab_row.h); rows it cannot certify take the
-// sorting path in the same workgroup.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kBlock) void sample_vocab_kernel(SampleArgs a) {
-  __shared__ union {
-    VocabLds v;
-    GenLds gen;
-  } L;
-  const uint32_t b = launch_row(a);
-  if (b >= a.B) return;
-  if (!a.row_cls_on && !(route_class(load_params(a, b), a.V) & a.row_class_mask)) return;
-  const bool vec4 = (reinterpret_cast<uintptr_t>(a.logits) % 16u == 0u) && (a.ld % 4u == 0u);
-  if (!vocab_row(a, b, L.v, vec4)) {
-    if (threadIdx.x == 0) atomicAdd(a.handovers, 1u);
-    __syncthreads();
-    general_row(a, b, L.gen, true);
-  }
-  LLMHIP_MARK(11);
 }
 
 // ---------------------------------------------------------------------------
@@ -134,13 +118,6 @@ hipError_t launch_slotmask(const SampleArgs& a, uint32_t* out, hipStream_t s) {
 // Calls without a count table (decode steps with one: fast_counts.hip).
 hipError_t launch_fast(const SampleArgs& a, bool vec, bool bigk, hipStream_t s) {
   return launch_fast_mode<false>(a, vec, bigk, s);
-}
-
-hipError_t launch_vocab(const SampleArgs& a, hipStream_t s) {
-  const uint32_t grid = launch_grid(a);
-  if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL(sample_vocab_kernel, dim3(grid), dim3(kBlock), 0, s, a);
-  return hipGetLastError();
 }
 
 hipError_t launch_seen_bits(const uint32_t* tokens, uint64_t n, uint32_t V, uint32_t* bits, hipStream_t s) {

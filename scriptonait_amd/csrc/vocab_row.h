@@ -1146,7 +1146,11 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
   return cut_and_walk(src);
 }
 
-// Returns false (uniformly) when the row must go to general_row.
+// Returns false (uniformly) when the row must go to general_row. PLAIN: the
+// call has no allowed mask, no ring and no row with a repetition penalty
+// and a history; that variant is compiled without the mask, penalty and
+// decode-step code (fewer values live through the passes).
+template <bool PLAIN>
 __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, VocabLds& L, bool vec4) {
   const uint32_t tid = threadIdx.x;
   LLMHIP_MARK(0);
@@ -1157,7 +1161,7 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   if (tid < kVMisc) L.misc[tid] = 0u;
 
   uint32_t h0 = 0, h1 = 0;
-  if (a.ring_cap) {
+  if (!PLAIN && a.ring_cap) {
     h0 = a.ring_len[b];
     h1 = ring_avail(a, b, h0);
     if (a.done && a.done[b]) {
@@ -1167,7 +1171,7 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
       }
       return true;
     }
-  } else if (a.hist && a.hist_offsets) {
+  } else if (!PLAIN && a.hist && a.hist_offsets) {
     h0 = a.hist_offsets[b];
     h1 = a.hist_offsets[b + 1];
   }
@@ -1175,9 +1179,9 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   const HistRow hr = hist_row(a, b, h0, h1);
   // The count table is kept current for the next step; this path counts the
   // window itself.
-  if (a.ring_cap && a.counts) counts_advance_all(a, b, len_b, hr.H);
+  if (!PLAIN && a.ring_cap && a.counts) counts_advance_all(a, b, len_b, hr.H);
   const float rp = P.repetition_penalty, T = P.temperature;
-  const bool use_pen = rp != 1.0f && hr.H > 0;
+  const bool use_pen = !PLAIN && rp != 1.0f && hr.H > 0;
   __syncthreads();
 
   // Repetition counts in an LDS hash (open addressing, probes bounded by the
@@ -1219,8 +1223,8 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   }
   // Each test on a row-wide condition is a branch of its own, so rows with
   // no mask, no penalty or T == 1 pay nothing per element for it.
-  const uint8_t* allowed = a.allowed;
-  const uint32_t* allowed_bits = a.allowed_bits;
+  const uint8_t* allowed = PLAIN ? nullptr : a.allowed;
+  const uint32_t* allowed_bits = PLAIN ? nullptr : a.allowed_bits;
   const uint32_t allowed_len = a.allowed_len, eos = a.eos_id;
   const bool div_t = T != 1.0f;
   auto wraw = [allowed, allowed_bits, allowed_len, eos, &L, use_pen](uint32_t i, float v)
