@@ -59,6 +59,9 @@ def parse_args():
                          "form each row's history")
     ap.add_argument("--counts", action="store_true",
                     help="with --decode-window: llmhip_decode_step_counts (incremental count table)")
+    ap.add_argument("--window-fill", choices=("own", "uniform"), default="own",
+                    help="with --decode-window: windows of the generations' own draws (a W-step warm-up) "
+                         "or of uniform ids (the ring starts with W + 50 of them)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -320,13 +323,16 @@ def bench_floor(args) -> None:
 
 def bench_decode(args) -> None:
     """llmhip_decode_step (or, with --counts, llmhip_decode_step_counts) on
-    the workload's rows as a decode loop: each row's ring starts with a
-    50-token prompt of uniform ids (capacity W + 1024), every step appends
-    the drawn id, and the history is the last W tokens. The untimed warm-up
-    runs W steps (at least --warmup), so the timed steps' windows hold the
-    generations' own draws: a row's recent top candidates, which the penalty
-    pushes below the register path's speculative threshold on some rows.
-    No generation ends (the end-of-text id is set past the vocabulary)."""
+    the workload's rows as a decode loop: every step appends the drawn id,
+    and the history is the ring's last W tokens (capacity W + 1024). With
+    --window-fill own (the default) each ring starts with a 50-token prompt
+    of uniform ids and the untimed warm-up runs W steps (at least --warmup),
+    so the timed steps' windows hold the generations' own draws: a row's
+    recent top candidates, repeated, which the penalty pushes below the
+    register path's speculative threshold on many rows. With uniform, each
+    ring starts with W + 50 uniform ids and the timed steps replace at most
+    --steps of the window's tokens. No generation ends (the end-of-text id
+    is set past the vocabulary)."""
     import torch
 
     from scriptonait_amd.sampler import Sampler
@@ -340,9 +346,11 @@ def bench_decode(args) -> None:
     stream = torch.cuda.current_stream(dev)
     sets = _rotating_sets(w, dev)
     rs = np.random.default_rng(W)
+    own = args.window_fill == "own"
+    pre = 50 if own else W + 50
     ring = torch.zeros((w.B, cap), dtype=torch.int32, device=dev)
-    ring[:, :50] = torch.from_numpy(rs.integers(0, w.V, size=(w.B, 50)).astype(np.int32)).to(dev)
-    ln = torch.full((w.B,), 50, dtype=torch.int32, device=dev)
+    ring[:, :pre] = torch.from_numpy(rs.integers(0, w.V, size=(w.B, pre)).astype(np.int32)).to(dev)
+    ln = torch.full((w.B,), pre, dtype=torch.int32, device=dev)
     done = torch.zeros(w.B, dtype=torch.int32, device=dev)
     rng = torch.from_numpy(w.rng_seeds.view(np.int64).copy()).to(dev)
     ids = torch.empty(w.B, dtype=torch.int32, device=dev)
@@ -353,7 +361,7 @@ def bench_decode(args) -> None:
     n = len(sets)
     no_eos = 0xFFFFFFFF
     steps = max(1, min(args.steps, 1000))
-    warmup = max(args.warmup, W)
+    warmup = max(args.warmup, W) if own else args.warmup
     us = _event_time_us(stream, lambda i: sampler.decode_step(sets[i % n], w.params, ring, ln, done, W, rng, ids,
                                                               V=w.V, eos_id=no_eos, stream=stream, counts=counts,
                                                               counted=counted),
@@ -363,10 +371,10 @@ def bench_decode(args) -> None:
         "metric": "decode step, us per step",
         "value": us, "unit": "us", "higher_is_better": False, "steps": steps, "warmup": warmup,
         "config": {"workload": f"{w.name}: {w.description}", "B": w.B, "V": w.V, "window": W,
-                   "count_table": bool(args.counts)},
+                   "count_table": bool(args.counts), "window_fill": args.window_fill},
         "rows_per_s": w.B / (us * 1e-6), "status_flags": st.flags, "handovers": st.handovers,
-        "dtype": "f32", "data": f"synthetic ({w.name}, {n} rotating device input sets; rings of a 50-id "
-                                f"uniform prompt (seed {W}) and the generations' own draws)",
+        "dtype": "f32", "data": f"synthetic ({w.name}, {n} rotating device input sets; rings of {pre} uniform ids "
+                                f"(seed {W})" + (" and the generations' own draws)" if own else ")"),
     }), flush=True)
     sampler.close()
 
