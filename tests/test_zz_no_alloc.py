@@ -87,11 +87,13 @@ def test_noalloc_matches_the_allocating_entry_twice_in_a_row(sampler):
     assert np.array_equal(second[1]["ids"], o2.ids)
     assert np.array_equal(second[1]["rng"], o2.rng_state)
 
-    print("no-alloc call 3: B=12, V=50257, top_k 40 and 1000 (the sorting path's select, keys in the array)",
-          flush=True)
+    print("no-alloc call 3: B=12, V=50257, top_k 40 (streaming kernel) and 2000 (the sorting path's select, "
+          "keys in the array)", flush=True)
     w3 = make_workload(4, B=12)
     prm3 = np.repeat(w3.params, w3.B)
-    prm3["top_k"] = np.where(np.arange(w3.B) % 2 == 0, 40, 1000)
+    # K = 2000 at V = 50257 is past what the streaming kernel's list holds, so
+    # those rows take the sorting path, whose keys live in the array.
+    prm3["top_k"] = np.where(np.arange(w3.B) % 2 == 0, 40, 2000)
     prm3["repetition_penalty"] = 1.1
     rs = np.random.default_rng(3)
     w3.hist = rs.integers(0, w3.V, size=w3.B * 300).astype(np.uint32)
