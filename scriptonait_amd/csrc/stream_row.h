@@ -10,9 +10,10 @@
 //     the previous row, before its tail); while they land, the history's
 //     multiplicities go into an LDS hash, with a bit filter so that only
 //     history ids probe it.
-//  2. positions past V and ids the allowed mask excludes become -inf
-//     (generate.rs:333-341); ids in the history are marked, their penalty
-//     left for later. Every thread counts the maxima of its groups of 8
+//  2. positions past V and ids the allowed mask excludes (generate.rs:333-341:
+//     their value is -inf) are set in a per-thread exclusion mask, never
+//     counted or listed; ids in the history are marked, their penalty left
+//     for later. Every thread counts the maxima of its groups of 8
 //     unmarked values into a fine key histogram (key bits 31..20).
 //  3. t0: the lower edge of the fine bin holding the K-th largest group
 //     maximum. At least K values that no penalty touches lie at or above
@@ -59,7 +60,7 @@ constexpr uint32_t kSEmpty = 0xffffffffu;
 constexpr uint32_t kSPend = 512;             // listed values waiting for their penalty
 
 // misc[] slots
-enum : uint32_t { kSCandN = 0, kSDistinct = 1, kSFull = 2, kSPendN = 3, kSMisc = 4 };
+enum : uint32_t { kSCandN = 0, kSDistinct = 1, kSFull = 2, kSPendN = 3, kSTau = 4, kSMisc = 5 };
 
 struct StreamLds {
   __attribute__((aligned(16))) uint32_t coarse[kCoarseBins];
@@ -274,12 +275,20 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
       return pm;
     };
     auto gmax = [&](const float (&buf)[kSNS * 4], uint32_t skip) __attribute__((always_inline)) {
+      // A wave none of whose values is skipped (no mask, no history id)
+      // takes plain maxima.
+      const bool any_skip = __ballot(skip != 0u) != 0ull;
 #pragma unroll
       for (int c = 0; c < (int)kSNS; c += 2) {
         float g = -INFINITY;
+        if (!any_skip) {
 #pragma unroll
-        for (int e = 4 * c; e < 4 * c + 8; ++e)
-          if (!((skip >> e) & 1u)) g = fmaxf(g, buf[e]);
+          for (int e = 4 * c; e < 4 * c + 8; ++e) g = fmaxf(g, buf[e]);
+        } else {
+#pragma unroll
+          for (int e = 4 * c; e < 4 * c + 8; ++e)
+            if (!((skip >> e) & 1u)) g = fmaxf(g, buf[e]);
+        }
         if (g > -INFINITY) atomicAdd(&L.fine[f2key(g) >> 20], 1u);
       }
     };
@@ -290,14 +299,13 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
     auto list_piece = [&](const float (&buf)[kSNS * 4], uint32_t p, uint32_t pm, uint32_t xm)
                           __attribute__((always_inline)) {
       const uint32_t tid = opaque_tid();
-      uint32_t hits = 0u, pen = 0u;
+      // The compares as one bit mask, then the exclusions and marks as
+      // whole-mask operations.
+      uint32_t ge = 0u;
 #pragma unroll
-      for (int e = 0; e < (int)kSNS * 4; ++e) {
-        const bool ge = buf[e] >= tf && !((xm >> e) & 1u);
-        const bool marked = (pm >> e) & 1u;
-        hits |= (ge && !marked ? 1u : 0u) << e;
-        pen |= (ge && marked ? 1u : 0u) << e;
-      }
+      for (int e = 0; e < (int)kSNS * 4; ++e) ge |= (buf[e] >= tf ? 1u : 0u) << e;
+      ge &= ~xm;
+      const uint32_t hits = ge & ~pm, pen = ge & pm;
       const uint32_t hc = (uint32_t)__popc(hits);
       const uint32_t inc = wave_incl_scan(hc);
       const uint32_t wt = readlane_u32(inc, 63);
@@ -345,9 +353,17 @@ __device__ __forceinline__ void stream_rows(const SampleArgs& a, StreamKernelLds
       lds_barrier();
       coarse_from_fine(L.fine, L.coarse);
       lds_barrier();
-      // 3. The threshold (the same in every wave).
-      const uint32_t t0 = hist_locate(L.coarse, L.fine, K, lane).lo;
-      const uint32_t tlo = t0 ? lower_past_ties(t0, T, lane) : 0u;
+      // 3. The threshold, selected by one wave (ahead of the others on its
+      //    SIMD) and published in LDS; 1 says the row is not bounded.
+      if (wave == 0u) {
+        __builtin_amdgcn_s_setprio(3);
+        const uint32_t t0 = hist_locate(L.coarse, L.fine, K, lane).lo;
+        const uint32_t t = t0 ? lower_past_ties(t0, T, lane) : 0u;
+        (void)lds_publish(&L.misc[kSTau], t ? t : 1u);
+        __builtin_amdgcn_s_setprio(0);
+      }
+      const uint32_t tpub = lds_wait_nonzero(&L.misc[kSTau], 1u, a);
+      const uint32_t tlo = tpub > 1u ? tpub : 0u;
       LLMHIP_MARK(3);
       if (tlo == 0u) {
         outcome = 1u;
