@@ -1253,7 +1253,14 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   };
   auto wval = [wraw, div_t, T](uint32_t i, float v) __attribute__((always_inline)) -> float {
     v = wraw(i, v);
-    if (div_t) v = v / T;  // generate.rs:357-359
+    if (div_t) {
+      // generate.rs:357-359. The empty asm keeps the division inside the
+      // (row-uniform) branch: left alone, the compiler computes it for every
+      // element and selects, which costs rows with T == 1 a division each.
+      float t = T;
+      asm volatile("" : "+v"(t));
+      v = v / t;
+    }
     return v;
   };
   const StreamSrc<decltype(wval)> src{row, V, vec4, wval};
