@@ -1227,7 +1227,7 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   const uint32_t* allowed_bits = PLAIN ? nullptr : a.allowed_bits;
   const uint32_t allowed_len = a.allowed_len, eos = a.eos_id;
   const bool div_t = T != 1.0f;
-  auto wraw = [allowed, allowed_bits, allowed_len, eos, &L, use_pen](uint32_t i, float v)
+  auto wraw = [=, &L](uint32_t i, float v)
       __attribute__((always_inline)) -> float {
     if (allowed) {  // generate.rs:333-341
       if (i < allowed_len && i != eos && allowed[i] == 0) v = -INFINITY;
