@@ -580,10 +580,13 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
     const float y = w - mx;
     const uint32_t k = vbucket(y);
     const uint32_t bi = L.binfo[k];
+    // The cheap term is computed while the bucket's word is read (the
+    // empty asm keeps it ahead of the class test that waits for the read).
+    const bool cheap = y >= -80.0f;
+    float ta = cheap ? cheap_x(y) * rcpS : 0.0f;
+    asm volatile("" : "+v"(ta));
     const uint32_t c0 = bcls(bi, 0), c1 = bcls(bi, 1);
     if (c0 == kBSkip && c1 == kBSkip) return;
-    const bool cheap = y >= -80.0f;
-    const float ta = cheap ? cheap_x(y) * rcpS : 0.0f;
     float t = -1.0f;  // the exact term, once computed
     if (thr > 0.0f) {
       bool in;
