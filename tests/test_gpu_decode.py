@@ -197,11 +197,14 @@ def test_decode_loop_greedy_drawing_its_own_top_ids(sampler):
 
 
 @pytest.mark.parametrize("counts", [False, True])
-def test_decode_loop_sorting_path_top_k(sampler, counts):
-    """V = 40000 top-k rows (beyond the register path's V): the sorting
-    path's select bound, list and merge sort inside a decode loop, with the
-    ring's window as the history (and the count table kept current)."""
-    _run(sampler, 40000, make_params(0.7, 50, 0.95, 0.05, 1.15), steps=12, B=8, window=256, cap=320,
+@pytest.mark.parametrize("k", [50, 2000])
+def test_decode_loop_large_vocab_top_k(sampler, counts, k):
+    """V = 40000 top-k rows (beyond the register path's V) inside a decode
+    loop, with the ring's window as the history (and the count table kept
+    current): top_k = 50 runs the streaming kernel's decode-step variant,
+    top_k = 2000 (more than its list holds at this V) the sorting path's
+    select bound, list and merge sort."""
+    _run(sampler, 40000, make_params(0.7, k, 0.95, 0.05, 1.15), steps=12, B=8, window=256, cap=320,
          max_prompt=200, counts=counts)
 
 
