@@ -1,10 +1,14 @@
 """GPU: top-k rows beyond the headline K against the oracle.
 
 Rows with 64 < top_k <= 4096 and V <= 32768 stay in the fast kernel's
-large-K variant. Rows it hands over (and larger V) select the K largest keys
-by a radix select in the sorting path and sort them in LDS; K > 4096 sorts
-the whole row in HBM scratch. All must give the reference's order: key
-descending, ties by ascending id (crates/llm-core/src/generate.rs:364-367).
+large-K variant. With V > 32768 the streaming kernel takes the K its list
+holds (top_k * ceil(V / 32768) * 5 <= 16384, penalty >= 1: here V = 40000
+with K = 50 or 1100, V = 50257 with K = 50, V = 131072 with K = 64); the
+sorting path takes larger K and the rows either kernel hands over: it
+selects the K largest keys from a bound (or a radix select) and sorts them
+in LDS, and K > 4096 sorts the whole row in HBM scratch. All must give the
+reference's order: key descending, ties by ascending id
+(crates/llm-core/src/generate.rs:364-367).
 """
 import numpy as np
 import pytest
@@ -26,8 +30,10 @@ def test_top_k_above_the_fast_limit(sampler, k):
 @pytest.mark.parametrize("V,k", [(32000, 1100), (32000, 3000), (40000, 50), (40000, 1100), (40000, 3000)])
 def test_top_k_select_with_ties_at_the_cut(sampler, V, k):
     """Logits on a coarse grid: the K-th key is shared by hundreds of ids, of
-    which only the lowest ids are kept (V = 40000: the sorting path's LDS
-    select, whose waves meet their ids in ascending order)."""
+    which only the lowest ids are kept (V = 40000: K = 50 and 1100 in the
+    streaming kernel, whose list keeps every id at the threshold; K = 3000
+    in the sorting path's LDS select, whose waves meet their ids in
+    ascending order)."""
     w = make_workload(3, B=16, V=V)
     w.logits[:] = np.round(w.logits * 2.0) / 2.0
     prm = make_params(1.3, k, 1.0, 0.0, 1.0)
@@ -39,10 +45,11 @@ def test_top_k_select_with_ties_at_the_cut(sampler, V, k):
 def test_sorting_path_select_fallbacks(sampler, case):
     """V = 40000 top-k rows whose bound cannot be used as is: T = 100 makes
     division merge runs of about 200 adjacent keys (longer than the tie
-    lowering covers), and logits on a grid of step 6 put thousands of ids on
-    the value at the bound (more candidates than the list holds). Both
-    divide every key and select exactly; ids, kept counts, probabilities and
-    RNG states match the oracle."""
+    lowering covers: the streaming kernel hands these K = 50 rows to the
+    sorting path in its own workgroup), and logits on a grid of step 6 put
+    thousands of ids on the value at the bound (more candidates than the
+    list holds). Both divide every key and select exactly; ids, kept counts,
+    probabilities and RNG states match the oracle."""
     w = make_workload(3, B=16, V=40000)
     if case == "long_tie_runs":
         prm = make_params(100.0, 50, 0.9, 0.0, 1.0)
