@@ -30,10 +30,11 @@ def test_top_k_above_the_fast_limit(sampler, k):
 @pytest.mark.parametrize("V,k", [(32000, 1100), (32000, 3000), (40000, 50), (40000, 1100), (40000, 3000)])
 def test_top_k_select_with_ties_at_the_cut(sampler, V, k):
     """Logits on a coarse grid: the K-th key is shared by hundreds of ids, of
-    which only the lowest ids are kept (V = 40000: K = 50 and 1100 in the
-    streaming kernel, whose list keeps every id at the threshold; K = 3000
-    in the sorting path's LDS select, whose waves meet their ids in
-    ascending order)."""
+    which only the lowest ids are kept (V = 40000: K = 50 and 1100 go to
+    the streaming kernel, which lists every id at its threshold or, when
+    they overflow its list, hands the row to the sorting path in its own
+    workgroup; K = 3000 goes to the sorting path's LDS select, whose waves
+    meet their ids in ascending order)."""
     w = make_workload(3, B=16, V=V)
     w.logits[:] = np.round(w.logits * 2.0) / 2.0
     prm = make_params(1.3, k, 1.0, 0.0, 1.0)
