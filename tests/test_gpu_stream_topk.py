@@ -159,3 +159,18 @@ def test_more_rows_than_the_class_table(sampler):
         prm[b] = kinds[b % 3]
     g = _device_run(sampler, w, prm, want_probs=False)
     _check(g, w, prm, "2100 rows", want_probs=False)
+
+
+@pytest.mark.parametrize("cfg,k", [(4, 40), (5, 50)])
+def test_full_batches_at_small_k(sampler, cfg, k):
+    """Configs 4 and 5 at their full batch (1024 rows of 50257, 512 rows of
+    131072 with penalized Zipf histories) with the reference's default
+    top_k (40) and 50: every row through the streaming kernel, bit-exact,
+    none handed over."""
+    w = make_workload(cfg)
+    prm = np.repeat(w.params, w.B)
+    prm["top_k"] = k
+    print(f"config {cfg} full batch B={w.B} k={k}", flush=True)
+    g = _device_run(sampler, w, prm, want_probs=False)
+    _check(g, w, prm, f"config{cfg} full k={k}", want_probs=False)
+    assert g["handovers"] == 0
