@@ -908,7 +908,7 @@ __device__ __forceinline__ bool fast_row(const SampleArgs& a, FastLds<NCH, BIGK>
     if (arrive < kTauWaves) {
       if (tm > -INFINITY) {  // a NaN or -inf maximum is not counted
         const uint32_t k = f2key(tm);
-        atomicAdd(&L.coarse[k >> 24], 1u);
+        bin_add_grouped(L.coarse, k >> 24);
         atomicAdd(&L.fine[k >> 20], 1u);
       }
       // kSyncSample counts the sample waves in bits 20 and up and the row

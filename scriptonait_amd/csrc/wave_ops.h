@@ -87,6 +87,18 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return lane == 0 ? 0ull : (~0ull >> (64u - lane));
 }
 
+// atomicAdd(&bins[bin], 1) for every active lane of the wave. The lanes that
+// share the first active lane's bin add as one atomic, so lanes whose bins
+// crowd one address do not serialize there.
+__device__ __forceinline__ void bin_add_grouped(uint32_t* bins, uint32_t bin) {
+  const uint64_t act = __ballot(true);
+  const uint32_t lead = (uint32_t)__ffsll((unsigned long long)act) - 1u;
+  const uint32_t b0 = readlane_u32(bin, lead);
+  const uint64_t m = __ballot(bin == b0);
+  if (bin != b0) atomicAdd(&bins[bin], 1u);
+  else if (lane_id() == lead) atomicAdd(&bins[b0], (uint32_t)__popcll(m));
+}
+
 // "Better" for the greedy argmax (crates/llm-core/src/ops/loss.rs:6-16):
 // larger value wins; equal values keep the smaller index.
 __device__ __forceinline__ void argmax_combine(float& bv, uint32_t& bi, float ov, uint32_t oi) {
