@@ -249,11 +249,14 @@ struct StreamSrc {
   }
   // Element i's post-temperature value.
   __device__ __forceinline__ float value_at(uint32_t i) const { return wval(i, row[i]); }
-  // Elements blk * 1024 .. blk * 1024 + 1023, by the calling wave.
+  // Blocks of 1024 elements (a wave takes one at a time: load_block).
   __device__ __forceinline__ uint32_t blocks() const { return (V + 1023u) / 1024u; }
-  template <class F>
-  __device__ __forceinline__ void for_each_block(F&& f, uint32_t blk) const {
+  // The calling lane's elements of block blk (16 of its 1024: the wave
+  // takes the block): values w, ids, and bit e of valid set for each that
+  // exists.
+  __device__ __forceinline__ void load_block(uint32_t blk, float (&w)[16], uint32_t (&id)[16], uint32_t& valid) const {
     const uint32_t lane = threadIdx.x & 63u;
+    valid = 0u;
     if (vec4) {
       const float4* r4 = reinterpret_cast<const float4*>(row);
       const uint32_t nq = (V + 3u) / 4u;
@@ -268,20 +271,25 @@ struct StreamSrc {
         const uint32_t i = 4u * (blk * 256u + lane + 64u * s);
         const float v[4] = {v4[s].x, v4[s].y, v4[s].z, v4[s].w};
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if (i + c < V) f(wval(i + c, v[c]), i + c);
+        for (int c = 0; c < 4; ++c) {
+          const bool in = i + c < V;
+          w[4 * s + c] = in ? wval(i + c, v[c]) : 0.0f;
+          id[4 * s + c] = i + c;
+          valid |= (in ? 1u : 0u) << (4 * s + c);
+        }
       }
     } else {
-      float v[16];
 #pragma unroll
       for (int s = 0; s < 16; ++s) {
         const uint32_t i = blk * 1024u + lane + 64u * s;
-        v[s] = i < V ? row[i] : 0.0f;
+        w[s] = i < V ? row[i] : 0.0f;
       }
 #pragma unroll
       for (int s = 0; s < 16; ++s) {
         const uint32_t i = blk * 1024u + lane + 64u * s;
-        if (i < V) f(wval(i, v[s]), i);
+        w[s] = i < V ? wval(i, w[s]) : 0.0f;
+        id[s] = i;
+        valid |= (i < V ? 1u : 0u) << s;
       }
     }
   }
@@ -305,18 +313,17 @@ struct ListSrc {
     for_each_part(f, 0u, kBlock);
   }
   __device__ __forceinline__ uint32_t blocks() const { return (n + 1023u) / 1024u; }
-  template <class F>
-  __device__ __forceinline__ void for_each_block(F&& f, uint32_t blk) const {
+  __device__ __forceinline__ void load_block(uint32_t blk, float (&w)[16], uint32_t (&id)[16], uint32_t& valid) const {
     const uint32_t lane = threadIdx.x & 63u;
-    uint2 e[16];
+    valid = 0u;
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       const uint32_t j = blk * 1024u + lane + 64u * s;
-      e[s] = j < n ? list[j] : make_uint2(0u, 0u);
+      const uint2 e = j < n ? list[j] : make_uint2(0u, 0u);
+      w[s] = key2f(e.x);
+      id[s] = e.y;
+      valid |= (j < n ? 1u : 0u) << s;
     }
-#pragma unroll
-    for (int s = 0; s < 16; ++s)
-      if (blk * 1024u + lane + 64u * s < n) f(key2f(e[s].x), e[s].y);
   }
 };
 
@@ -783,8 +790,34 @@ __device__ __forceinline__ bool run_folds(FoldSpec (&fs)[NF], float mx, float u,
       if (lane == 0) blk = atomicAdd(&L.misc[kVSplitNext], 1u);
       blk = readlane_u32(blk, 0);
       if (blk >= nb) break;
-      if (from_list) tl.for_each_block(split, blk);
-      else src.for_each_block(split, blk);
+      // Only about 2% of the elements lie in tie buckets, but a wave would
+      // run the tie work for an element position whenever one lane's
+      // element there does. The lane's tie-bucket elements are found
+      // first, then taken one at a time: the wave runs the tie work as many
+      // times as its busiest lane has such elements.
+      float w[16];
+      uint32_t id[16], valid;
+      if (from_list) tl.load_block(blk, w, id, valid);
+      else src.load_block(blk, w, id, valid);
+      uint32_t todo = 0u;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if (!((valid >> e) & 1u)) continue;
+        const uint32_t bi = L.binfo[vbucket(w[e] - mx)];
+        todo |= (bcls(bi, 0) == kBTie || bcls(bi, 1) == kBTie) ? 1u << e : 0u;
+      }
+      while (todo != 0u) {
+        const uint32_t e = (uint32_t)__builtin_ctz(todo);
+        todo &= todo - 1u;
+        float we = w[0];
+        uint32_t ie = id[0];
+#pragma unroll
+        for (int q = 1; q < 16; ++q) {
+          we = e == (uint32_t)q ? w[q] : we;
+          ie = e == (uint32_t)q ? id[q] : ie;
+        }
+        split(we, ie);
+      }
     }
     lds_signal(&L.misc[kVSplitDone]);
   }
