@@ -194,17 +194,112 @@ __device__ __forceinline__ double block_scan_f64(double x, double* tmp, double& 
 // Row streamed from memory by every pass: float4 groups, two batches of 4
 // per thread in flight (the next batch loads while this one is visited), or
 // scalars when the row is not 16-byte aligned.
-template <class WV>
+//
+// VP gives an element's value in parts: pre(i, v) the allowed mask, pen()
+// whether the row has penalized history ids, hit(i) / hit4(i) their filter
+// bits, hist(i, v) the penalized value of a history id (v when i is not
+// one), post(v) the division by T. History ids are about 1% of a row, but a
+// wave looking one up at every element position where one of its lanes
+// holds one would look up at almost every position: each lane's history
+// ids among its 16 elements are looked up one at a time instead (finish).
+template <class VP>
 struct StreamSrc {
   const float* row;
   uint32_t V;
   bool vec4;
-  WV wval;
-  // Threads t0 .. t0 + nt - 1 visit the row between them (the caller's
-  // thread is one of them).
+  VP vp;
+  // Element i's value from its logit v.
+  __device__ __forceinline__ float value(uint32_t i, float v) const {
+    v = vp.pre(i, v);
+    if (vp.pen() && vp.hit(i)) v = vp.hist(i, v);
+    return vp.post(v);
+  }
+  // w holds pre() of the lane's 16 elements (ids id_of(e)); hm marks the
+  // history ids among them. Their values are replaced, then post() applied
+  // to every valid element.
+  template <class IdOf>
+  __device__ __forceinline__ void finish(float (&w)[16], uint32_t valid, uint32_t hm, IdOf&& id_of) const {
+    while (hm != 0u) {
+      const uint32_t e = (uint32_t)__builtin_ctz(hm);
+      hm &= hm - 1u;
+      float we = w[0];
+#pragma unroll
+      for (int q = 1; q < 16; ++q) we = e == (uint32_t)q ? w[q] : we;
+      we = vp.hist(id_of(e), we);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) w[q] = e == (uint32_t)q ? we : w[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if ((valid >> q) & 1u) w[q] = vp.post(w[q]);
+  }
+  // Elements 4 * (q0 + t + kBlock * s) + c of float4 groups cur[s], s < 4:
+  // their pre() values, validity and history marks.
+  __device__ __forceinline__ void pre_quads(const float4 (&v4)[4], uint32_t base, uint32_t stride, float (&w)[16],
+                                            uint32_t& valid, uint32_t& hm) const {
+    valid = 0u;
+    hm = 0u;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t i = 4u * (base + stride * (uint32_t)s);
+      const float v[4] = {v4[s].x, v4[s].y, v4[s].z, v4[s].w};
+      const uint32_t hb = vp.pen() ? vp.hit4(i) : 0u;  // one filter word holds the four ids
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bool in = i + c < V;
+        w[4 * s + c] = in ? vp.pre(i + c, v[c]) : 0.0f;
+        valid |= (in ? 1u : 0u) << (4 * s + c);
+        hm |= (in && ((hb >> c) & 1u) ? 1u : 0u) << (4 * s + c);
+      }
+    }
+  }
   template <class F>
-  __device__ __forceinline__ void for_each_part(F&& f, uint32_t t0, uint32_t nt) const {
-    const uint32_t t = threadIdx.x - t0;
+  __device__ __forceinline__ void for_each(F&& f) const {
+    const uint32_t t = threadIdx.x;
+    constexpr uint32_t nt = kBlock;
+    if (!vp.pen()) {
+      // No history ids: each element's value as it is visited.
+      if (vec4) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+        const uint32_t nq = (V + 3u) / 4u;
+        float4 cur[4], nxt[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const uint32_t q = t + nt * s;
+          cur[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        for (uint32_t q0 = 0; q0 < nq; q0 += 4u * nt) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const uint32_t q = q0 + 4u * nt + t + nt * s;
+            nxt[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const uint32_t i = 4u * (q0 + t + nt * s);
+            const float v[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (i + c < V) f(vp.post(vp.pre(i + c, v[c])), i + c);
+          }
+#pragma unroll
+          for (int s = 0; s < 4; ++s) cur[s] = nxt[s];
+        }
+      } else {
+        uint32_t i = t;
+        for (; i + 7u * nt < V; i += 8u * nt) {
+          float v[8];
+#pragma unroll
+          for (int s = 0; s < 8; ++s) v[s] = row[i + nt * s];
+#pragma unroll
+          for (int s = 0; s < 8; ++s) f(vp.post(vp.pre(i + nt * s, v[s])), i + nt * s);
+        }
+        for (; i < V; i += nt) f(vp.post(vp.pre(i, row[i])), i);
+      }
+      return;
+    }
+    float w[16];
+    uint32_t valid, hm;
     if (vec4) {
       const float4* r4 = reinterpret_cast<const float4*>(row);
       const uint32_t nq = (V + 3u) / 4u;
@@ -220,35 +315,40 @@ struct StreamSrc {
           const uint32_t q = q0 + 4u * nt + t + nt * s;
           nxt[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+        pre_quads(cur, q0 + t, nt, w, valid, hm);
+        finish(w, valid, hm, [&](uint32_t e) { return 4u * (q0 + t + nt * (e >> 2)) + (e & 3u); });
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const uint32_t i = 4u * (q0 + t + nt * s);
-          const float v[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (i + c < V) f(wval(i + c, v[c]), i + c);
-        }
+        for (int e = 0; e < 16; ++e)
+          if ((valid >> e) & 1u) f(w[e], 4u * (q0 + t + nt * (uint32_t)(e >> 2)) + (uint32_t)(e & 3));
 #pragma unroll
         for (int s = 0; s < 4; ++s) cur[s] = nxt[s];
       }
     } else {
-      uint32_t i = t;
-      for (; i + 7u * nt < V; i += 8u * nt) {
-        float v[8];
+      for (uint32_t i0 = t; i0 < V; i0 += 16u * nt) {
 #pragma unroll
-        for (int s = 0; s < 8; ++s) v[s] = row[i + nt * s];
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t i = i0 + nt * e;
+          w[e] = i < V ? row[i] : 0.0f;
+        }
+        valid = 0u;
+        hm = 0u;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) f(wval(i + nt * s, v[s]), i + nt * s);
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t i = i0 + nt * e;
+          const bool in = i < V;
+          w[e] = in ? vp.pre(i, w[e]) : 0.0f;
+          valid |= (in ? 1u : 0u) << e;
+          hm |= (in && vp.pen() && vp.hit(i) ? 1u : 0u) << e;
+        }
+        finish(w, valid, hm, [&](uint32_t e) { return i0 + nt * e; });
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if ((valid >> e) & 1u) f(w[e], i0 + nt * (uint32_t)e);
       }
-      for (; i < V; i += nt) f(wval(i, row[i]), i);
     }
   }
-  template <class F>
-  __device__ __forceinline__ void for_each(F&& f) const {
-    for_each_part(f, 0u, kBlock);
-  }
   // Element i's post-temperature value.
-  __device__ __forceinline__ float value_at(uint32_t i) const { return wval(i, row[i]); }
+  __device__ __forceinline__ float value_at(uint32_t i) const { return value(i, row[i]); }
   // Blocks of 1024 elements (a wave takes one at a time: load_block).
   __device__ __forceinline__ uint32_t blocks() const { return (V + 1023u) / 1024u; }
   // The calling lane's elements of block blk (16 of its 1024: the wave
@@ -256,7 +356,7 @@ struct StreamSrc {
   // exists.
   __device__ __forceinline__ void load_block(uint32_t blk, float (&w)[16], uint32_t (&id)[16], uint32_t& valid) const {
     const uint32_t lane = threadIdx.x & 63u;
-    valid = 0u;
+    uint32_t hm;
     if (vec4) {
       const float4* r4 = reinterpret_cast<const float4*>(row);
       const uint32_t nq = (V + 3u) / 4u;
@@ -267,30 +367,41 @@ struct StreamSrc {
         v4[s] = q < nq ? r4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint32_t i = 4u * (blk * 256u + lane + 64u * s);
-        const float v[4] = {v4[s].x, v4[s].y, v4[s].z, v4[s].w};
+      for (int e = 0; e < 16; ++e) id[e] = 4u * (blk * 256u + lane + 64u * (uint32_t)(e >> 2)) + (uint32_t)(e & 3);
+      if (!vp.pen()) {
+        valid = 0u;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bool in = i + c < V;
-          w[4 * s + c] = in ? wval(i + c, v[c]) : 0.0f;
-          id[4 * s + c] = i + c;
-          valid |= (in ? 1u : 0u) << (4 * s + c);
+        for (int s = 0; s < 4; ++s) {
+          const float v[4] = {v4[s].x, v4[s].y, v4[s].z, v4[s].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const bool in = id[4 * s + c] < V;
+            w[4 * s + c] = in ? vp.post(vp.pre(id[4 * s + c], v[c])) : 0.0f;
+            valid |= (in ? 1u : 0u) << (4 * s + c);
+          }
         }
+        return;
       }
+      pre_quads(v4, blk * 256u + lane, 64u, w, valid, hm);
+      finish(w, valid, hm, [&](uint32_t e) { return 4u * (blk * 256u + lane + 64u * (e >> 2)) + (e & 3u); });
     } else {
 #pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const uint32_t i = blk * 1024u + lane + 64u * s;
-        w[s] = i < V ? row[i] : 0.0f;
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t i = blk * 1024u + lane + 64u * e;
+        w[e] = i < V ? row[i] : 0.0f;
       }
+      valid = 0u;
+      hm = 0u;
 #pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const uint32_t i = blk * 1024u + lane + 64u * s;
-        w[s] = i < V ? wval(i, w[s]) : 0.0f;
-        id[s] = i;
-        valid |= (i < V ? 1u : 0u) << s;
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t i = blk * 1024u + lane + 64u * e;
+        const bool in = i < V;
+        w[e] = in ? vp.pre(i, w[e]) : 0.0f;
+        id[e] = i;
+        valid |= (in ? 1u : 0u) << e;
+        hm |= (in && vp.pen() && vp.hit(i) ? 1u : 0u) << e;
       }
+      finish(w, valid, hm, [&](uint32_t e) { return blk * 1024u + lane + 64u * e; });
     }
   }
 };
@@ -1186,6 +1297,55 @@ __device__ __forceinline__ bool vocab_folds(const SampleArgs& a, uint32_t b, uin
 // call has no allowed mask, no ring and no row with a repetition penalty
 // and a history; that variant is compiled without the mask, penalty and
 // decode-step code (fewer values live through the passes).
+// An element's value in parts (StreamSrc): the allowed mask
+// (generate.rs:333-341), the penalized value of a history id (the mask, then
+// one penalty step per occurrence, generate.rs:343-352, computed once per id
+// into the LDS hash), and the division by T (generate.rs:357-359).
+struct VocabVals {
+  const uint8_t* allowed;
+  const uint32_t* allowed_bits;
+  uint32_t allowed_len, eos;
+  bool use_pen;
+  const VocabLds* L;
+  bool div;
+  float T;
+  __device__ __forceinline__ float pre(uint32_t i, float v) const {
+    if (allowed) {
+      if (i < allowed_len && i != eos && allowed[i] == 0) v = -INFINITY;
+    }
+    if (allowed_bits) {
+      if (i < allowed_len && i != eos && ((allowed_bits[i >> 5] >> (i & 31u)) & 1u) == 0u) v = -INFINITY;
+    }
+    return v;
+  }
+  __device__ __forceinline__ bool pen() const { return use_pen; }
+  __device__ __forceinline__ bool hit(uint32_t i) const { return (L->hbits[(i >> 5) & (kVBits - 1u)] >> (i & 31u)) & 1u; }
+  // Filter bits of ids i .. i + 3 (i a multiple of 4: one word holds them).
+  __device__ __forceinline__ uint32_t hit4(uint32_t i) const { return (L->hbits[(i >> 5) & (kVBits - 1u)] >> (i & 31u)) & 15u; }
+  // The filter holds ids modulo 2^17, so a hit may be no history id: v stays.
+  __device__ __forceinline__ float hist(uint32_t i, float v) const {
+    uint32_t h = (i * 2654435761u) >> 21;
+    for (uint32_t probe = 0; probe < kVHash; ++probe) {
+      const uint32_t k = L->hkey[h];
+      if (k == i) return L->hval[h];
+      if (k == kHashEmpty) break;
+      h = (h + 1u) & (kVHash - 1u);
+    }
+    return v;
+  }
+  __device__ __forceinline__ float post(float v) const {
+    if (div) {
+      // The empty asm keeps the division inside the (row-uniform) branch:
+      // left alone, the compiler computes it for every element and selects,
+      // which costs rows with T == 1 a division each.
+      float t = T;
+      asm volatile("" : "+v"(t));
+      v = v / t;
+    }
+    return v;
+  }
+};
+
 template <bool PLAIN>
 __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, VocabLds& L, bool vec4) {
   const uint32_t tid = threadIdx.x;
@@ -1259,48 +1419,13 @@ __device__ __forceinline__ bool vocab_row(const SampleArgs& a, uint32_t b, Vocab
   }
   // Each test on a row-wide condition is a branch of its own, so rows with
   // no mask, no penalty or T == 1 pay nothing per element for it.
-  const uint8_t* allowed = PLAIN ? nullptr : a.allowed;
-  const uint32_t* allowed_bits = PLAIN ? nullptr : a.allowed_bits;
-  const uint32_t allowed_len = a.allowed_len, eos = a.eos_id;
   const bool div_t = T != 1.0f;
-  auto wraw = [=, &L](uint32_t i, float v)
-      __attribute__((always_inline)) -> float {
-    if (allowed) {  // generate.rs:333-341
-      if (i < allowed_len && i != eos && allowed[i] == 0) v = -INFINITY;
-    }
-    if (allowed_bits) {
-      if (i < allowed_len && i != eos && ((allowed_bits[i >> 5] >> (i & 31u)) & 1u) == 0u) v = -INFINITY;
-    }
-    if (use_pen) {
-      if ((L.hbits[(i >> 5) & (kVBits - 1u)] >> (i & 31u)) & 1u) {
-        uint32_t h = (i * 2654435761u) >> 21;
-        for (uint32_t probe = 0; probe < kVHash; ++probe) {
-          const uint32_t k = L.hkey[h];
-          if (k == i) {
-            v = L.hval[h];
-            break;
-          }
-          if (k == kHashEmpty) break;
-          h = (h + 1u) & (kVHash - 1u);
-        }
-      }
-    }
-    return v;
-  };
-  auto wval = [wraw, div_t, T](uint32_t i, float v) __attribute__((always_inline)) -> float {
-    v = wraw(i, v);
-    if (div_t) {
-      // generate.rs:357-359. The empty asm keeps the division inside the
-      // (row-uniform) branch: left alone, the compiler computes it for every
-      // element and selects, which costs rows with T == 1 a division each.
-      float t = T;
-      asm volatile("" : "+v"(t));
-      v = v / t;
-    }
-    return v;
-  };
-  const StreamSrc<decltype(wval)> src{row, V, vec4, wval};
-  const StreamSrc<decltype(wraw)> raw{row, V, vec4, wraw};
+  const VocabVals vv{PLAIN ? nullptr : a.allowed, PLAIN ? nullptr : a.allowed_bits, a.allowed_len, a.eos_id,
+                     use_pen, &L, div_t, T};
+  VocabVals vr = vv;
+  vr.div = false;
+  const StreamSrc<VocabVals> src{row, V, vec4, vv};
+  const StreamSrc<VocabVals> raw{row, V, vec4, vr};
   const bool defer = div_t && T >= 0x1p-126f && T < INFINITY;
   return vocab_folds(a, b, len_b, P, L, src, raw, defer ? T : 0.0f);
 }
