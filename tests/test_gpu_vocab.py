@@ -132,6 +132,34 @@ def test_repetition_penalty_histories(sampler, rp):
     _assert_same(g, o, f"penalty {rp}")
 
 
+@pytest.mark.parametrize("top_k", [0, 40])
+def test_history_filter_aliases_above_2_17(sampler, top_k):
+    """V > 2^17: the history filter holds ids modulo 2^17, so an id that is
+    not in the history can share its bit with one that is (id + 2^17). Such
+    ids are raised to the top of their rows, so that taking one for a history
+    id (penalizing it, or dropping it) would change the ids; top_k = 0 runs
+    the full-vocabulary kernel, top_k = 40 the streaming kernel."""
+    rs = np.random.default_rng(11)
+    B, V, H = 8, 140000, 600
+    logits = rs.normal(0, 1.5, (B, V)).astype(np.float32)
+    hist = rs.integers(0, V, size=(B, H)).astype(np.uint32)
+    hist[:, :40] = rs.integers(1 << 17, V, size=(B, 40))  # ids whose filter bits alias low ids
+    for b in range(B):
+        alias = hist[b, :40] - (1 << 17)
+        alias = alias[~np.isin(alias, hist[b])]  # low ids that only share a bit
+        logits[b, alias[:10]] = 7.0 + rs.random(min(10, alias.size)).astype(np.float32)
+        logits[b, hist[b, :5]] = 7.5  # and history ids at the top too
+    offs = (np.arange(B + 1) * H).astype(np.uint32)
+    prm = make_params(0.9, top_k, 0.95, 0.02, 1.3)
+    seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
+    g, o = _both(sampler, logits, prm, seeds, hist.reshape(-1), offs, V=V)
+    _assert_same(g, o, f"filter aliases top_k={top_k}")
+    if top_k == 0:
+        assert g.extra["handovers"] == 0
+    # (At top_k = 40 this wide-tailed data lists more than the streaming
+    # kernel's 512 slots on some rows, which the sorting path then samples.)
+
+
 def test_rows_the_kernel_hands_to_the_sorting_path(sampler):
     """NaN and +inf logits, an all -inf row and a history longer than the
     LDS count table: these rows take the sorting path inside the kernel."""
