@@ -190,14 +190,25 @@ def test_allowed_mask_full_vocab(sampler):
     _assert_same(g, o, "allowed mask")
 
 
+@pytest.mark.parametrize("rp", [1.0, 1.3])
 @pytest.mark.parametrize("V,ld", [(1001, 1003), (8191, 8193), (40000, 40001)])
-def test_rows_with_an_odd_stride(sampler, V, ld):
-    """ld % 4 != 0 (and odd V): the kernel reads the row with dword loads."""
+def test_rows_with_an_odd_stride(sampler, V, ld, rp):
+    """ld % 4 != 0 (and odd V): the kernel reads the row with dword loads;
+    with rp = 1.3, over a history that repeats its ids and raises some of
+    them to the top, the history ids are looked up in that path too."""
     rs = np.random.default_rng(V)
-    B = 12
+    B, H = 12, 300
     logits = np.full((B, ld), 1e30, dtype=np.float32)  # padding past V must never be read as logits
     logits[:, :V] = rs.normal(0, 2, (B, V)).astype(np.float32)
-    prm = make_params(0.9, 0, 0.95, 0.0, 1.0)
+    hist = offs = None
+    if rp != 1.0:
+        hist = rs.integers(0, V, size=(B, H)).astype(np.uint32)
+        hist[:, ::5] = hist[:, :1]  # one id many times per row
+        for b in range(B):
+            logits[b, hist[b, :8]] = 9.0
+        hist = hist.reshape(-1)
+        offs = (np.arange(B + 1) * H).astype(np.uint32)
+    prm = make_params(0.9, 0, 0.95, 0.0, rp)
     seeds = rs.integers(0, 2**63, size=B, dtype=np.uint64)
-    g, o = _both(sampler, logits, prm, seeds, V=V)
-    _assert_same(g, o, f"odd stride V={V} ld={ld}")
+    g, o = _both(sampler, logits, prm, seeds, hist, offs, V=V)
+    _assert_same(g, o, f"odd stride V={V} ld={ld} rp={rp}")
